@@ -1,0 +1,153 @@
+"""Build the KDA operator libraries in-tree for gfx950.
+
+Two shared libraries land in the Python package directory
+(``sgl_glm53_ascend_ops/``):
+
+* ``libkda_amd.so`` -- the HIP kernels and the C ABI declared in
+  ``include/kda_abi.h``; depends only on the HIP runtime (loadable from ctypes);
+* ``sgl_glm53_ascend_ops_lib.so`` -- the torch operator layer
+  (``TORCH_LIBRARY(sgl_glm53_ascend)``), linked against ``libkda_amd.so``
+  through ``$ORIGIN``. The name is the reference's (``PKG/CMakeLists.txt:197-204``),
+  so its loader convention carries over.
+
+Run ``python 01-glm53-ascend_amd/kda_build.py``; every invocation recompiles.
+hipcc cross-compiles for gfx950 on a host without a GPU.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import sysconfig
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+PKG = os.path.join(HERE, "sgl_glm53_ascend_ops")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = os.environ.get("KDA_OFFLOAD_ARCH", "gfx950")
+
+HIP_SOURCES = ["kda_recurrent.hip", "kda_chunk.hip"]
+ABI_SOURCES = ["kda_abi.cpp"]
+TORCH_SOURCES = ["kda_torch_ops.cpp"]
+
+# Packed-FP32 VALU forms are disabled for all device code: they are not
+# needed for throughput here and some of their forms have misbehaved on this
+# hardware pool.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in proc.stdout.splitlines() if "packed-fp32-ops" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out, flush=True)
+
+
+def _torch_flags():
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    incs = ce.include_paths(device_type="cuda")
+    libs = ce.library_paths(device_type="cuda")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cflags = [f"-I{p}" for p in incs] + [
+        f"-I{sysconfig.get_paths()['include']}",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DUSE_ROCM=1",
+        "-D__HIP_PLATFORM_AMD__=1",
+        "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-std=c++17",
+        "-O2",
+        "-fPIC",
+        "-Wall",
+        "-Wno-unused-variable",
+    ]
+    ldflags = [f"-L{p}" for p in libs] + [
+        "-lc10",
+        "-lc10_hip",
+        "-ltorch",
+        "-ltorch_cpu",
+        "-ltorch_hip",
+        f"-L{ROCM}/lib",
+        "-lamdhip64",
+    ]
+    return cflags, ldflags
+
+
+def _atomic_link(cmd_without_output, dst, verbose):
+    fd, tmp = tempfile.mkstemp(prefix=os.path.basename(dst) + ".", suffix=".tmp", dir=PKG)
+    os.close(fd)
+    try:
+        _run(cmd_without_output + ["-o", tmp], verbose)
+        os.replace(tmp, dst)
+    finally:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+
+
+def build(verbose: bool = False) -> None:
+    os.makedirs(PKG, exist_ok=True)
+    with tempfile.TemporaryDirectory(prefix="kda_build_") as obj_dir:
+        procs = []
+        objs = []
+        for src in HIP_SOURCES + ABI_SOURCES:
+            obj = os.path.join(obj_dir, src + ".o")
+            objs.append(obj)
+            lang = [] if src.endswith(".hip") else ["-x", "hip"]
+            cmd = [HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *lang, "-c",
+                   os.path.join(CSRC, src), "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                stderr=subprocess.STDOUT, text=True)))
+        for cmd, p in procs:
+            out, _ = p.communicate()
+            out = "\n".join(l for l in out.splitlines() if "packed-fp32-ops" not in l)
+            if p.returncode != 0:
+                raise RuntimeError(f"command failed ({p.returncode}): {' '.join(cmd)}\n{out}")
+            if verbose and out.strip():
+                print(out, flush=True)
+        lib_abi = os.path.join(PKG, "libkda_amd.so")
+        _atomic_link([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs], lib_abi, verbose)
+
+        cflags, ldflags = _torch_flags()
+        tobjs = []
+        for src in TORCH_SOURCES:
+            obj = os.path.join(obj_dir, src + ".o")
+            _run(["g++", *cflags, f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj],
+                 verbose)
+            tobjs.append(obj)
+        lib_ops = os.path.join(PKG, "sgl_glm53_ascend_ops_lib.so")
+        _atomic_link(
+            ["g++", "-shared", "-fPIC", *tobjs, f"-L{PKG}", "-lkda_amd",
+             "-Wl,-rpath,$ORIGIN", *ldflags],
+            lib_ops,
+            verbose,
+        )
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print("built", os.path.join(PKG, "libkda_amd.so"), "and sgl_glm53_ascend_ops_lib.so")

@@ -1,0 +1,258 @@
+"""Benchmark of the KDA hot path on one MI355X: decode tok/s + state HBM GB/s, prefill tok/s.
+
+Workload (BASELINE.json ``configs[1]``, the configuration the metric is quoted
+on): varlen recurrent decode, one token for each of 256 sequences, H=32,
+K=V=128, bf16 q/k/v (q, k L2-normalized), fp32 per-channel log decay
+``g = logsigmoid(randn)`` and ``beta = sigmoid(randn)``, fp32 state pool of 512
+slots (``randn*0.05``, K-contiguous), ``state_indices`` a seeded random
+permutation of 256 of the slots, updated in place. One *step* is one call of
+the decode operator over the whole batch (every step advances all 256
+sequences by one token in place). ``value`` = tokens/s = 256 / step time.
+
+Also reported (same JSON line): the chunked prefill of ``configs[2]`` (T=8192
+single sequence, H=32, K=V=128, chunk 64) as ``prefill``, the decode kernel's
+roofline (algorithmic bytes / kernel time, measured with HIP events on the
+launch stream), and the CPU baseline (this repository's torch oracle of the
+reference CPU path, on the host cores, over a bounded sample).
+
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "01-glm53-ascend_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+BF16_PEAK_TFLOPS = 2500.0  # MI355X published dense bf16 MFMA
+
+# Config 2 (decode) shape.
+DEC_N, DEC_H, DEC_D, DEC_SLOTS = 256, 32, 128, 512
+# Algorithmic bytes per token-head: state read + write (2*D*D*4), q, k, v
+# (3*D*2), g (D*4), beta (4), o (D*2).
+BYTES_PER_TOKEN_HEAD = 2 * DEC_D * DEC_D * 4 + 3 * DEC_D * 2 + DEC_D * 4 + 4 + DEC_D * 2
+# + cu_seqlens (257 x 4) + indices (256 x 4) + ... as quoted: 2052 B of metadata.
+DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
+
+# Config 3 (prefill) shape.
+PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
+# Dense-tile FLOPs per token-head: 2*(5*BT*D + 3*D*D).
+PF_FLOP = PF_T * PF_H * 2 * (5 * PF_BT * PF_D + 3 * PF_D * PF_D)
+# Algorithmic bytes: q,k,v bf16 in, g fp32, beta fp32, o bf16 out, final state fp32 out.
+PF_BYTES = PF_T * PF_H * (3 * PF_D * 2 + PF_D * 4 + 4 + PF_D * 2) + PF_H * PF_D * PF_D * 4
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def decode_inputs(device):
+    from tests import kda_cases as C
+
+    perm = torch.randperm(DEC_SLOTS, generator=C.gen(2))[:DEC_N].tolist()
+    case = C.prepared_case(DEC_H, (1,) * DEC_N, D=DEC_D, slots=DEC_SLOTS, indices=perm, seed=2)
+    return case
+
+
+def run_decode(steps, warmup, device="cuda"):
+    from tests import kda_cases as C
+
+    ops = torch.ops.sgl_glm53_ascend
+    case = decode_inputs(device)
+    q, k, v, g, beta = (getattr(case, n).to(device) for n in ("q", "k", "v", "g", "beta"))
+    pool = C.to_dev(case.pool, device)
+    idx = case.indices.to(device)
+    cu = case.cu_seqlens.to(device)
+
+    def step():
+        return ops.kda_prepared_varlen_recurrent(
+            q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
+            cu_seqlens=cu, scale=case.scale)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / steps
+    kernel_us = ev0.elapsed_time(ev1) * 1e3 / steps
+    return dict(ms_per_step=ms_step, kernel_us=kernel_us)
+
+
+def run_prefill(steps, warmup, device="cuda"):
+    from tests import kda_cases as C
+
+    ops = torch.ops.sgl_glm53_ascend
+    case = C.prepared_case(PF_H, (PF_T,), D=PF_D, slots=2, indices=[1], seed=3, zero_pool=True)
+    q, k, v, g, beta = (getattr(case, n).to(device) for n in ("q", "k", "v", "g", "beta"))
+    pool = C.to_dev(case.pool, device)
+    idx = case.indices.to(device)
+    cu = case.cu_seqlens.to(device)
+
+    def step():
+        pool.zero_()  # zero initial state each step (config 3)
+        return ops.kda_prepared_varlen_chunk(
+            q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
+            cu_seqlens=cu, scale=case.scale)
+
+    try:
+        step()
+        torch.cuda.synchronize()
+    except RuntimeError as e:
+        _log(f"prefill unavailable: {str(e).splitlines()[0]}")
+        return None
+    for _ in range(warmup):
+        step()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / steps
+    gpu_us = ev0.elapsed_time(ev1) * 1e3 / steps
+    return dict(ms_per_step=ms_step, gpu_us=gpu_us)
+
+
+def cpu_baseline(budget_s=10.0):
+    """The oracle's recurrent decode (the reference CPU path's loop structure,
+    bench/kda_chunk/kda_python.py:253-307) on the host cores."""
+    from oracle import kda_ref as R
+    from tests import kda_cases as C
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    sample_n = 64
+    case = C.prepared_case(DEC_H, (1,) * sample_n, D=DEC_D, slots=sample_n + 1, seed=2)
+    qs = case.q.float() * case.scale
+
+    def once():
+        pool = C.clone_pool(case.pool)
+        t0 = time.perf_counter()
+        R.kda_recurrent(qs, case.k, case.v, case.g, case.beta, state_pool=pool,
+                        state_indices=case.indices, cu_seqlens=case.cu_seqlens)
+        return time.perf_counter() - t0
+
+    once()  # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 50):
+        times.append(once())
+    med = statistics.median(times)
+    return dict(
+        value=sample_n / med,
+        unit="tok/s",
+        cores=torch.get_num_threads(),
+        kind="port",
+        sample=(f"oracle kda_recurrent (torch fp32, CPU) on {sample_n} of the 256 config-2 "
+                f"sequences x 1 token, H={DEC_H}, K=V={DEC_D}; median of {len(times)} runs; "
+                f"os.cpu_count()={os.cpu_count()}"),
+    )
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workload")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
+              "(the KDA path shards by head and sequence with no exchange; see DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    import sgl_glm53_ascend_ops  # noqa: F401
+
+    _log("decode: config 2 (B=256, H=32, K=V=128)")
+    dec = run_decode(args.steps, args.warmup)
+    tok_s = DEC_N / (dec["ms_per_step"] / 1e3)
+    achieved = DEC_BYTES / (dec["kernel_us"] * 1e-6) / 1e9
+    _log(f"decode: {dec['ms_per_step']*1e3:.1f} us/step, kernel {dec['kernel_us']:.1f} us, "
+         f"{achieved:.0f} GB/s")
+
+    prefill = None
+    if not args.no_prefill:
+        _log("prefill: config 3 (T=8192, H=32, K=V=128, chunk 64)")
+        pf = run_prefill(max(3, args.steps // 5), max(1, args.warmup // 5))
+        if pf is not None:
+            tf = PF_FLOP / (pf["gpu_us"] * 1e-6) / 1e12
+            prefill = dict(
+                workload="chunk prefill T=8192 H=32 K=V=128 BT=64 bf16 qkv, fp32 g/beta/state",
+                tok_per_s=PF_T / (pf["ms_per_step"] / 1e3),
+                ms_per_step=pf["ms_per_step"],
+                gpu_us=pf["gpu_us"],
+                tflops=tf,
+                mfma_frac=tf / BF16_PEAK_TFLOPS,
+                hbm_gbs=PF_BYTES / (pf["gpu_us"] * 1e-6) / 1e9,
+                attainable_frac=(tf * 1e12) / min(BF16_PEAK_TFLOPS * 1e12,
+                                                  HBM_PEAK_GBS * 1e9 * PF_FLOP / PF_BYTES),
+            )
+            _log(f"prefill: {pf['ms_per_step']*1e3:.1f} us/step, {tf:.1f} TFLOP/s")
+
+    cpu = None
+    if not args.no_cpu:
+        _log("cpu baseline: oracle decode on host cores")
+        cpu = cpu_baseline()
+        _log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+
+    line = dict(
+        metric="KDA decode tok/s + state HBM GB/s (B=256); chunk prefill tok/s (T=8k)",
+        value=tok_s,
+        unit="tok/s",
+        n_gpus=1,
+        steps=args.steps,
+        warmup=args.warmup,
+        ms_per_step=dec["ms_per_step"],
+        higher_is_better=True,
+        scaling="weak",
+        vs_baseline=None,
+        dtype="fp32",
+        data="synthetic",
+        config=dict(
+            workload=("varlen recurrent decode B=256 x 1 token, H=32, K=V=128, bf16 q/k/v, "
+                      "fp32 log-decay g and beta, fp32 K-contiguous state pool of 512 slots "
+                      "updated in place (BASELINE configs[1])"),
+            batch=DEC_N, heads=DEC_H, head_dim=DEC_D, pool_slots=DEC_SLOTS,
+        ),
+        state_hbm_gbs=achieved,
+        roofline=dict(
+            bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
+            frac=achieved / HBM_PEAK_GBS, traffic=None,
+            kernel="recurrent_kernel<128,16,bf16,bf16,LOG>",
+            algorithmic_bytes_per_launch=DEC_BYTES, kernel_us=dec["kernel_us"],
+        ),
+        prefill=prefill,
+        cpu_baseline=cpu,
+    )
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

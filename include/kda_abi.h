@@ -1,0 +1,183 @@
+/*
+ * kda_abi.h -- C ABI of the MI355X (gfx950) KDA operator library.
+ *
+ * Plain C: POD argument structs, raw device pointers, element strides, and a
+ * `void *` HIP stream. No torch, no HIP headers, so the library can be bound
+ * from ctypes / cffi / another host language without a C++ toolchain.
+ *
+ * These entry points replace the reference's host->device launch seam:
+ *
+ *   kda_recurrent_launch  replaces LaunchKdaDecodeH16/H32/H64 and
+ *                         LaunchKdaPrefillH4/H8
+ *                         (sgl-glm53-ascend-ops/csrc/kda/recurrent/
+ *                          kda_varlen_recurrent.h:363-367), with the argument
+ *                         block KdaLaunchArgs (same file, :328-361), and the
+ *                         prepared-input kernels behind prepared_recurrent
+ *                         (csrc/kda/prepared_recurrent.cpp:592-602,676-708);
+ *   kda_chunk_launch      replaces LaunchKdaVarlenChunk
+ *                         (csrc/kda/chunk/kda_varlen_chunk_kernel.cpp:1641-1662),
+ *                         argument block KdaChunkLaunchArgs
+ *                         (csrc/kda/chunk/kda_varlen_chunk.h:120-141);
+ *   kda_chunk_workspace_bytes  sizes the chunk op's scratch, the analogue of
+ *                         kWorkspaceFloatsPerBlock (kda_varlen_chunk.h:79-116).
+ *
+ * Layout contract (same as the reference ops):
+ *   token tensors   [T, H, D] contiguous (the leading batch dim of the torch
+ *                   op's [1, T, H, D] is 1);
+ *   beta / b        [T, H];
+ *   state pool      logical [slots, H, K, V], K contiguous: element
+ *                   (s, h, k, v) lives at
+ *                   state[s*state_stride_slot + h*state_stride_head + v*D + k];
+ *   slot 0          the padding row: read as a zero state, never written;
+ *   cu_seqlens      int32 [N+1], non-decreasing, cu_seqlens[N] <= T;
+ *   indices         int32 [N]; entries outside [0, num_slots) are treated as
+ *                   slot 0 (the kernels never address outside the pool).
+ *
+ * All launches are asynchronous on `stream` and never synchronize the host.
+ * Every function returns a KdaStatus (0 = success).
+ */
+#ifndef KDA_ABI_H
+#define KDA_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KDA_ABI_VERSION 1
+
+typedef enum KdaStatus {
+    KDA_OK = 0,
+    KDA_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, misalignment */
+    KDA_ERR_UNSUPPORTED = 2,      /* a shape / dtype / mode with no kernel */
+    KDA_ERR_LAUNCH = 3,           /* the HIP runtime refused the launch */
+    KDA_ERR_WORKSPACE = 4         /* workspace missing or too small */
+} KdaStatus;
+
+typedef enum KdaDType {
+    KDA_BF16 = 0,
+    KDA_F32 = 1
+} KdaDType;
+
+/* How the per-channel decay and beta arrive.
+ *   RAW    gate = bf16 `a` [T,H,D], beta = bf16 logit `b` [T,H]; the kernel
+ *          computes g = lower_bound * sigmoid(exp(A_log[h]) * (a + dt_bias)),
+ *          beta = sigmoid(b), and L2-normalizes q and k (the sglang schema,
+ *          kda_varlen_recurrent.cpp:257-265);
+ *   LOG    gate = fp32 log decay g [T,H,D] (<= 0), beta = fp32 [T,H];
+ *   DECAY  gate = fp32 multiplicative decay exp(g) [T,H,D], beta = fp32 [T,H]
+ *          (the prepared_recurrent schema, prepared_recurrent.cpp:715-720). */
+typedef enum KdaGateMode {
+    KDA_GATE_RAW = 0,
+    KDA_GATE_LOG = 1,
+    KDA_GATE_DECAY = 2
+} KdaGateMode;
+
+typedef struct KdaRecurrentArgs {
+    const void *q;        /* [T,H,D], qk_dtype */
+    const void *k;        /* [T,H,D], qk_dtype */
+    const void *v;        /* [T,H,D], v_dtype */
+    const void *gate;     /* see KdaGateMode */
+    const void *beta;     /* see KdaGateMode */
+    const float *A_log;   /* [H], RAW only */
+    const float *dt_bias; /* [H*D], RAW only */
+
+    float *state;               /* pool base, see layout contract */
+    int64_t state_stride_slot;  /* elements */
+    int64_t state_stride_head;  /* elements */
+    int64_t num_slots;
+
+    const int32_t *state_indices; /* [N] */
+    const int32_t *cu_seqlens;    /* [N+1] */
+    void *out;                    /* [T,H,D], v_dtype; every token written */
+
+    /* Per-step checkpoints [rows, steps, H, K, V], K contiguous (null = off).
+     * Row = the request's position n, step = its local token index; written
+     * after each step's update when slot > 0, and the final write-back to
+     * the pool is then skipped (decode.h:45-49,683-708,743-751). */
+    float *intermediate;
+    int64_t mid_stride_req;  /* elements */
+    int64_t mid_stride_step; /* elements */
+    int64_t mid_stride_head; /* elements */
+    int64_t mid_rows;
+    int64_t mid_steps;
+
+    /* Prefix tracking (null = off): slot track_indices[n] (> 0) receives the
+     * state after track_lens[n] of the request's tokens; 0 = initial state. */
+    const int32_t *track_indices; /* [N] */
+    const int32_t *track_lens;    /* [N] */
+
+    float scale;       /* multiplies q after the optional L2 norm */
+    float lower_bound; /* RAW only */
+    int32_t num_seqs;
+    int32_t num_tokens;
+    int32_t num_heads;   /* H: heads per token row and per pool slot */
+    int32_t head_begin;  /* first head processed (0 = all from the start) */
+    int32_t head_count;  /* heads processed from head_begin (0 = to H) */
+    int32_t head_dim;    /* K == V; 64 or 128 */
+    int32_t qk_dtype;  /* KdaDType */
+    int32_t v_dtype;   /* KdaDType, also the output dtype */
+    int32_t gate_mode; /* KdaGateMode */
+    int32_t qk_l2norm; /* LOG mode: normalize q and k in the kernel */
+} KdaRecurrentArgs;
+
+/* Fused recurrent (token-by-token) KDA over packed varlen sequences. */
+int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream);
+
+typedef struct KdaChunkArgs {
+    const void *q;        /* [T,H,D], qk_dtype */
+    const void *k;        /* [T,H,D], qk_dtype */
+    const void *v;        /* [T,H,D], v_dtype */
+    const void *gate;     /* RAW: bf16 a; LOG: fp32 g  (DECAY is unsupported) */
+    const void *beta;     /* RAW: bf16 b; LOG: fp32 beta */
+    const float *A_log;   /* [H], RAW only */
+    const float *dt_bias; /* [H*D], RAW only */
+
+    float *state;
+    int64_t state_stride_slot;
+    int64_t state_stride_head;
+    int64_t num_slots;
+
+    const int32_t *state_indices; /* [N] */
+    const int32_t *cu_seqlens;    /* [N+1]; any lengths (no multiple-of-64 rule) */
+    void *out;                    /* [T,H,D], v_dtype */
+
+    const int32_t *track_indices; /* [N] or null */
+    const int32_t *track_lens;    /* [N] or null */
+
+    float scale;
+    float lower_bound;
+    int32_t num_seqs;
+    int32_t num_tokens;
+    int32_t num_heads;
+    int32_t head_dim;  /* 128 */
+    int32_t qk_dtype;
+    int32_t v_dtype;
+    int32_t gate_mode;
+    int32_t qk_l2norm;
+} KdaChunkArgs;
+
+/* Bytes of device scratch kda_chunk_launch needs for these arguments. An
+ * upper bound that depends only on T, N, H and D (no device reads). */
+size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
+                                 int32_t num_heads, int32_t head_dim);
+
+/* Chunked (chunk = 64 tokens) KDA over packed varlen sequences. `workspace`
+ * must hold kda_chunk_workspace_bytes(...) bytes of device memory; its
+ * contents need no initialization. */
+int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/* Human-readable text of a KdaStatus. */
+const char *kda_status_string(int status);
+
+/* KDA_ABI_VERSION of the built library. */
+int kda_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_ABI_H */
