@@ -35,6 +35,18 @@ __device__ __forceinline__ float4 load4(const float *p) {
     return *reinterpret_cast<const float4 *>(p);
 }
 
+typedef float kda_v4f __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming (nontemporal) access for data touched once per launch.
+__device__ __forceinline__ float4 load4_stream(const float *p) {
+    const kda_v4f t = __builtin_nontemporal_load(reinterpret_cast<const kda_v4f *>(p));
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ void store4_stream(float *p, float4 v) {
+    const kda_v4f t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<kda_v4f *>(p));
+}
+
 __device__ __forceinline__ float load1(const uint16_t *p) { return bf16_to_f32(*p); }
 __device__ __forceinline__ float load1(const float *p) { return *p; }
 

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
         const float *src = a.state + slot * a.state_stride_slot + head_off;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            S[p] = load4(src + static_cast<int64_t>(row0 + p * RPP) * D + 4 * kc);
+            S[p] = load4_stream(src + static_cast<int64_t>(row0 + p * RPP) * D + 4 * kc);
         }
     } else {
 #pragma unroll
@@ -97,11 +97,13 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
             track_len = a.track_lens[n];
         }
     }
+    // State tiles are touched once per launch: streamed with nontemporal
+    // loads and stores so they do not evict the token rows from the caches
+    // (measured ~10% more HBM throughput than cached accesses).
     auto store_state = [&](float *dst) {
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            *reinterpret_cast<float4 *>(dst + static_cast<int64_t>(row0 + p * RPP) * D + 4 * kc) =
-                S[p];
+            store4_stream(dst + static_cast<int64_t>(row0 + p * RPP) * D + 4 * kc, S[p]);
         }
     };
     if (track_slot > 0 && track_len == 0) {
@@ -240,6 +242,7 @@ KernelFn pick_np(int np) {
     if constexpr (D == 128) {
         switch (np) {
             case 16: return recurrent_kernel<D, 16, TQK, TV, GATE>;
+            case 8: return recurrent_kernel<D, 8, TQK, TV, GATE>;
             case 4: return recurrent_kernel<D, 4, TQK, TV, GATE>;
             case 1: return recurrent_kernel<D, 1, TQK, TV, GATE>;
             default: return nullptr;
@@ -339,12 +342,14 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
     if (kargs.head_count == 0 || kargs.head_begin + kargs.head_count > kargs.num_heads) {
         kargs.head_count = kargs.num_heads - kargs.head_begin;
     }
-    // V-split: one workgroup per (sequence, head) once that alone gives a few
-    // waves of workgroups over the 256 CUs; split value rows otherwise.
+    // V-split: two workgroups per (sequence, head) (64 value rows each, 32 KB
+    // of state per workgroup -- measured faster than one 64 KB workgroup at
+    // B=256, H=32) once that gives a few waves of workgroups over the 256 CUs;
+    // smaller row tiles otherwise.
     const int64_t pairs = static_cast<int64_t>(a.num_seqs) * kargs.head_count;
     int np;
     if (D == 128) {
-        np = pairs >= 1024 ? 16 : (pairs >= 128 ? 4 : 1);
+        np = pairs >= 1024 ? 8 : (pairs >= 128 ? 4 : 1);
     } else {
         np = pairs >= 2048 ? 4 : 1;
     }

@@ -245,7 +245,7 @@ def main():
         roofline=dict(
             bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
             frac=achieved / HBM_PEAK_GBS, traffic=None,
-            kernel="recurrent_kernel<128,16,bf16,bf16,LOG>",
+            kernel="recurrent_kernel<128,8,bf16,bf16,LOG>",
             algorithmic_bytes_per_launch=DEC_BYTES, kernel_us=dec["kernel_us"],
         ),
         prefill=prefill,

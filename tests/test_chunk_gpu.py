@@ -1,0 +1,186 @@
+"""GPU parity of the chunked prefill (bf16 MFMA, fp32 state) against the oracle.
+
+Small cases follow the reference's own chunk suite (tests/ops/test_kda_chunk.py:
+202-249): one and several chunks, several sequences, the zero slot, every
+position of the tracked checkpoint, untouched slots; plus what this build adds:
+sequence lengths that are not a multiple of 64 (the reference rejects them,
+:245-249). They are checked against the CPU oracle's chunked form
+(``oracle.kda_ref.kda_chunk``, the restatement of kda_python.py:41-188).
+
+BASELINE configs 3, 4 and 5 run at full size. At those sizes the CPU oracle
+would take minutes, so the reference there is this build's recurrent kernel
+run in fp32 (bf16 inputs widened exactly; that kernel is itself pinned to the
+oracle at <= 1e-5 by test_recurrent_gpu.py) -- the chunk == recurrent identity
+the reference cross-checks its own anchors with (kda_python.py:312-344).
+"""
+
+import pytest
+import torch
+
+from oracle import kda_ref as R
+from tests import kda_cases as C
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _oracle_chunk(case, pool_cpu):
+    qn, kn, g, beta = R.kda_prepare(case.A_log, case.a, case.dt_bias, case.q, case.k, case.b,
+                                    case.lower_bound, case.scale)
+    return R.kda_chunk(qn, kn, case.v, g, beta, state_pool=pool_cpu, state_indices=case.indices,
+                       cu_seqlens=case.cu_seqlens, track_state_indices=case.track_indices,
+                       track_state_lens=case.track_lens, out_dtype=torch.float32)
+
+
+def _run_chunk(ops, case, index_dtype=torch.int32):
+    pool = C.to_dev(case.pool, DEV)
+    out = ops.kda_varlen_chunk(prefill=True, **case.kwargs(DEV, pool=pool, index_dtype=index_dtype))
+    torch.cuda.synchronize()
+    return out, pool
+
+
+# (label, heads, cu_seqlens lengths, slots, track) -- test_kda_chunk.py:203-214
+REF_CASES = [
+    ("one chunk", 1, (64,), [1], None),
+    ("two chunks", 1, (128,), [1], None),
+    ("four chunks", 2, (256,), [1], None),
+    ("two sequences", 2, (128, 128), [1, 2], None),
+    ("ragged varlen", 1, (64, 128, 64), [1, 2, 3], None),
+    ("zero slot", 1, (128,), [0], None),
+    ("track at 0", 2, (128,), [1], ([4], [0])),
+    ("track mid-chunk", 2, (128,), [1], ([4], [32])),
+    ("track on boundary", 2, (128,), [1], ([4], [64])),
+    ("track at end", 1, (192,), [1], ([4], [192])),
+    # beyond the reference: lengths that are not a multiple of 64
+    ("unaligned 100", 1, (100,), [1], None),
+    ("unaligned varlen", 3, (1, 37, 100, 64, 130), [1, 2, 3, 0, 5], None),
+    ("track in ragged tail", 2, (100, 37), [1, 2], ([6, 0], [90, 3])),
+    ("track end of ragged", 2, (100,), [1], ([6], [100])),
+]
+
+
+@pytest.mark.parametrize("label,heads,lengths,slots,track", REF_CASES,
+                         ids=[c[0].replace(" ", "-") for c in REF_CASES])
+def test_chunk_matches_oracle(gpu_ops, label, heads, lengths, slots, track):
+    case = C.raw_case(heads, lengths, indices=slots, slots=8, seed=20261103 + len(label),
+                      track=track)
+    out, pool = _run_chunk(gpu_ops, case)
+    ref_pool = C.clone_pool(case.pool)
+    ref = _oracle_chunk(case, ref_pool)
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, f"{label} output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, f"{label} pool")
+    touched = set(s for s in slots if s > 0)
+    if track is not None:
+        touched |= set(s for s in track[0] if s > 0)
+    other = [s for s in range(8) if s not in touched]
+    assert torch.equal(pool.cpu()[other], case.pool[other]), "an unindexed slot was written"
+
+
+def test_chunk_leaves_other_slots_untouched(gpu_ops):
+    case = C.raw_case(2, (128,), indices=[3], slots=8, seed=3)
+    _, pool = _run_chunk(gpu_ops, case)
+    got = pool.cpu()
+    other = [s for s in range(8) if s != 3]
+    assert torch.equal(got[other], case.pool[other])
+    assert not torch.equal(got[3], case.pool[3])
+
+
+def test_chunk_index_dtypes_bit_identical(gpu_ops):
+    case = C.raw_case(4, (257, 64), indices=[3, 1], slots=6, seed=5, track=([5, 0], [64, 0]))
+    base_out, base_pool = _run_chunk(gpu_ops, case)
+    out, pool = _run_chunk(gpu_ops, case, index_dtype=torch.int64)
+    assert out.float().abs().sum().item() > 0
+    assert torch.equal(out, base_out)
+    assert torch.equal(pool.cpu(), base_pool.cpu())
+
+
+def test_chunk_tokens_outside_sequences_are_zero(gpu_ops):
+    case = C.raw_case(2, (70, 30), slots=4, seed=8)
+    T = case.q.shape[1]
+    case.cu_seqlens = torch.tensor([0, 70, T - 5], dtype=torch.int32)
+    torch.full((1, T, 2, 128), float("nan"), device=DEV, dtype=torch.bfloat16)
+    out, _ = _run_chunk(gpu_ops, case)
+    out = out.cpu()
+    assert torch.equal(out[0, T - 5:], torch.zeros_like(out[0, T - 5:]))
+    ref_pool = C.clone_pool(case.pool)
+    C.assert_out(out, _oracle_chunk(case, ref_pool), C.OUT_TOL, "output")
+
+
+def test_chunk_sequences_are_independent(gpu_ops):
+    case = C.raw_case(2, (70, 90, 40), slots=5, seed=9)
+    out1, _ = _run_chunk(gpu_ops, case)
+    case.v = case.v.clone()
+    case.v[0, 160:] += 1.0
+    out2, _ = _run_chunk(gpu_ops, case)
+    assert torch.equal(out1[0, :160], out2[0, :160])
+    assert not torch.equal(out1[0, 160:], out2[0, 160:])
+
+
+# --- prepared gates, BASELINE configs -----------------------------------------
+
+
+def _prepared_dev(case):
+    return {n: getattr(case, n).to(DEV) for n in ("q", "k", "v", "g", "beta")}
+
+
+def _chunk_prepared(ops, case, pool, dev):
+    out = ops.kda_prepared_varlen_chunk(
+        dev["q"], dev["k"], dev["v"], dev["g"], dev["beta"], initial_state_source=pool,
+        initial_state_indices=case.indices.to(DEV), cu_seqlens=case.cu_seqlens.to(DEV),
+        scale=case.scale)
+    torch.cuda.synchronize()
+    return out
+
+
+def _recurrent_fp32(ops, case, pool, dev):
+    """This build's recurrent kernel with fp32 I/O (exact widening of bf16)."""
+    out = ops.kda_prepared_varlen_recurrent(
+        dev["q"].float(), dev["k"].float(), dev["v"].float(), dev["g"], dev["beta"],
+        initial_state_source=pool, initial_state_indices=case.indices.to(DEV),
+        cu_seqlens=case.cu_seqlens.to(DEV), scale=case.scale)
+    torch.cuda.synchronize()
+    return out
+
+
+def test_prepared_chunk_matches_oracle_small(gpu_ops):
+    case = C.prepared_case(4, (300, 64, 1, 129), slots=6, indices=[1, 0, 3, 5], seed=31)
+    dev = _prepared_dev(case)
+    pool = C.to_dev(case.pool, DEV)
+    out = _chunk_prepared(gpu_ops, case, pool, dev)
+    ref_pool = C.clone_pool(case.pool)
+    ref = R.kda_chunk(case.q.float() * case.scale, case.k, case.v, case.g, case.beta,
+                      state_pool=ref_pool, state_indices=case.indices,
+                      cu_seqlens=case.cu_seqlens, out_dtype=torch.float32)
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, "output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
+
+
+@pytest.mark.parametrize(
+    "name,heads,lengths,slots,indices,gate",
+    [
+        # config 3: T=8192 single sequence, H=32, zero initial state
+        ("config3", 32, (8192,), 2, [1], (1.0, 0.0)),
+        # config 4: 16 sequences, lengths uniform in [1, 4096], 64-slot pool
+        ("config4", 32, None, 64, None, (1.0, 0.0)),
+        # config 5 (prefill half): T=65536, H=16, harsh decay
+        ("config5", 16, (65536,), 2, [1], (2.0, -2.0)),
+    ],
+)
+def test_baseline_configs_chunk_vs_recurrent(gpu_ops, name, heads, lengths, slots, indices, gate):
+    if lengths is None:
+        g_ = C.gen(4)
+        lengths = tuple(int(x) for x in torch.randint(1, 4097, (16,), generator=g_))
+        indices = torch.randperm(64, generator=g_)[:16].tolist()
+    case = C.prepared_case(heads, lengths, slots=slots, indices=indices, seed=len(name) + 3,
+                           gate_scale=gate[0], gate_shift=gate[1],
+                           zero_pool=(name != "config4"))
+    dev = _prepared_dev(case)
+    pool_c = C.to_dev(case.pool, DEV)
+    pool_r = C.to_dev(case.pool, DEV)
+    out_c = _chunk_prepared(gpu_ops, case, pool_c, dev)
+    out_r = _recurrent_fp32(gpu_ops, case, pool_r, dev)
+    e_o = C.assert_out(out_c.cpu(), out_r.cpu(), C.OUT_TOL, f"{name} output")
+    e_s = C.assert_rel(pool_c.cpu(), pool_r.cpu(), C.STATE_TOL, f"{name} final states")
+    print(f"{name}: output err {e_o:.2e}, state err {e_s:.2e}")
+    assert torch.isfinite(out_c.float()).all()
