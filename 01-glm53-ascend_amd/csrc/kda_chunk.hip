@@ -115,12 +115,13 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 __device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) { return __builtin_bit_cast(u32x4, v); }
 
-// x[8] -> bf16 hi (+ lo) fragments.
+// x[8] -> bf16 hi (+ lo) fragments; lo = bf16(x - hi), so x = hi + lo to
+// about 2^-17 relative.
 __device__ __forceinline__ bf16x8 to_bf16x8(const float x[8]) {
     u32x4 h;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        h[p] = pack2(f32_to_bf16(x[2 * p]), f32_to_bf16(x[2 * p + 1]));
+        h[p] = pack_bf16x2(x[2 * p], x[2 * p + 1]);
     }
     return as_bf16x8(h);
 }
@@ -128,12 +129,11 @@ __device__ __forceinline__ void split_bf16x8(const float x[8], bf16x8 &hi, bf16x
     u32x4 h, l;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const uint16_t h0 = f32_to_bf16(x[2 * p]);
-        const uint16_t h1 = f32_to_bf16(x[2 * p + 1]);
-        const uint16_t l0 = f32_to_bf16(x[2 * p] - bf16_to_f32(h0));
-        const uint16_t l1 = f32_to_bf16(x[2 * p + 1] - bf16_to_f32(h1));
-        h[p] = pack2(h0, h1);
-        l[p] = pack2(l0, l1);
+        const uint32_t hp = pack_bf16x2(x[2 * p], x[2 * p + 1]);
+        const float h0 = __uint_as_float(hp << 16);
+        const float h1 = __uint_as_float(hp & 0xffff0000u);
+        h[p] = hp;
+        l[p] = pack_bf16x2(x[2 * p] - h0, x[2 * p + 1] - h1);
     }
     hi = as_bf16x8(h);
     lo = as_bf16x8(l);
@@ -144,6 +144,13 @@ __device__ __forceinline__ void store_frag(char *base, int off, int idx, int lan
 }
 __device__ __forceinline__ bf16x8 load_frag(const char *base, int off, int idx, int lane) {
     return as_bf16x8(reinterpret_cast<const u32x4 *>(base + off)[idx * 64 + lane]);
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// accesses, not for its outstanding global loads (a full __syncthreads() also
+// drains vmcnt, which would stall the scan's prefetch of the next chunk).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ void seq_bounds(const KdaChunkArgs &a, int n, int &bos, int &eos) {
@@ -193,24 +200,43 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
 
 // ---------------------------------------------------------------------------
 // K1: per (chunk, head) intra-chunk work.
+//
+// 68 KiB of LDS, so two workgroups share a CU and one's loads overlap the
+// other's math. k is kept as its bf16 input plus a per-row inverse norm, q
+// never enters LDS (each wave loads its own rows into registers), and the
+// solve's X and v^T reuse the cumsum tile once it is dead.
 // ---------------------------------------------------------------------------
 
 constexpr int kPadF = 132;  // fp32 row stride of [64][128] tiles (bank spread)
-constexpr int kPadV = 72;   // u16 row stride of [128][64] transposed tiles
-constexpr int kPadX = 68;   // fp32 row stride of [64][64] tiles
+constexpr int kPadK = 136;  // bf16 row stride of the k tile
+constexpr int kPadX = 68;   // fp32 row stride of [64][64] tiles (16-B rows)
+
+// [128][64] bf16 tiles stored with 8-element groups XOR-swizzled by the row,
+// so the 16 rows a wave reads at one column land in different banks.
+__device__ __forceinline__ int swz(int row, int col) {
+    return row * 64 + ((((col >> 3) ^ (row & 7)) << 3) | (col & 7));
+}
 
 struct PrepShared {
-    float G[BT][kPadF];         // cumsum of the log decay
-    float K[BT][kPadF];         // normalized k
-    float Q[BT][kPadF];         // normalized, scaled q; later e^G k (bf16, [k][t])
-    uint16_t Vt[DK][kPadV];     // v^T, bf16 bits
-    float L[BT][BT + 1];        // diag(beta) strict-lower Akk
-    float X[BT][kPadX];         // (I + L)^-1, then T = X diag(beta)
+    union {
+        float G[BT][kPadF];  // cumsum of the log decay (S1-S4)
+        struct {
+            float X[BT][kPadX];       // (I + L)^-1, then T = X diag(beta) (S5-S6)
+            uint16_t Vt[DK * BT];     // v^T, bf16 bits, swizzled (S5-S6)
+        } late;
+    } r0;
+    union {
+        uint16_t K[BT][kPadK];   // k, bf16 input bits (S1-S4)
+        uint16_t KE[DK * BT];    // (e^G k)^T as bf16, swizzled (S4-S6)
+    } r1;
+    float LT[BT][kPadX];  // L^T: LT[j][i] = beta_i Akk[i][j] (j < i)
     float beta[BT];
+    float rnk[BT];        // k row scale (1 / norm, or 1)
     float carry[DK];
 };
+static_assert(sizeof(PrepShared) <= 80 * 1024, "two prepare workgroups per CU");
 
-template <typename TIn, int GATE>
+template <int GATE>
 __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkArgs a, char *ws,
                                                                  int nrec) {
     __shared__ PrepShared sm;
@@ -245,84 +271,100 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     const int r = lane & 15;
     const int gq = lane >> 4;
     char *rec = ws + LY.recs + (static_cast<size_t>(c) * H + h) * kRecBytes;
+    const bool norm = GATE == KDA_GATE_RAW || a.qk_l2norm != 0;
+    const uint16_t *qp = static_cast<const uint16_t *>(a.q);
 
-    // ---- S1: load rows (zero-padded), gates, norms -------------------------
+    // Row blocks I this wave builds Akk/Aqk pairs for (balanced over waves):
+    //   wave 0: (0,0) (1,0) (1,1)   wave 1: (2,0) (2,1) (2,2)
+    //   wave 2: (3,0) (3,1)         wave 3: (3,2) (3,3)
+    const int nI = wave == 0 ? 2 : 1;
+    const int I0 = wave == 0 ? 0 : (wave == 1 ? 2 : 3);
+    // Its q rows, loaded now so the loads overlap S1/S2: lane (r, gq) holds
+    // q[16I + r][32s + kperm(gq, e)] as 4 x (4 bf16) per slice pair.
+    uint2 qraw[2][4][2];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const int t = 16 * (I0 + ii) + r;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            qraw[ii][s][0] = make_uint2(0u, 0u);
+            qraw[ii][s][1] = make_uint2(0u, 0u);
+            if (ii < nI && t < len) {
+                const uint16_t *row = qp + (static_cast<int64_t>(t0 + t) * H + h) * DK + 32 * s;
+                qraw[ii][s][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
+                qraw[ii][s][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
+            }
+        }
+    }
+
+    // ---- S1: k rows, log decay, beta (zero-padded); L^T cleared -------------
     {
         const int kc = tid & 31;
         const int rg = tid >> 5;
-        const TIn *qp = static_cast<const TIn *>(a.q);
-        const TIn *kp = static_cast<const TIn *>(a.k);
-        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
-        const bool norm = GATE == KDA_GATE_RAW || a.qk_l2norm != 0;
+        const uint16_t *kp = static_cast<const uint16_t *>(a.k);
         float expA = 0.f;
         float4 dtb = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (GATE == KDA_GATE_RAW) {
             expA = expf(a.A_log[h]);
             dtb = load4(a.dt_bias + static_cast<int64_t>(h) * DK + 4 * kc);
         }
-#pragma unroll 2
+        uint2 kraw[8];
+        float4 g4[8];
+#pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int t = rg + 8 * i;
-            const bool valid = t < len;
             const int64_t base = (static_cast<int64_t>(t0 + t) * H + h) * DK + 4 * kc;
-            float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, g4 = q4;
-            uint2 vraw = make_uint2(0u, 0u);
-            if (valid) {
-                q4 = load4(qp + base);
-                k4 = load4(kp + base);
-                vraw = *reinterpret_cast<const uint2 *>(vp + base);
+            kraw[i] = make_uint2(0u, 0u);
+            g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < len) {
+                kraw[i] = *reinterpret_cast<const uint2 *>(kp + base);
                 if constexpr (GATE == KDA_GATE_RAW) {
                     const float4 av = load4(static_cast<const uint16_t *>(a.gate) + base);
                     const float lb = a.lower_bound;
-                    g4.x = lb / (1.0f + expf(-(expA * (av.x + dtb.x))));
-                    g4.y = lb / (1.0f + expf(-(expA * (av.y + dtb.y))));
-                    g4.z = lb / (1.0f + expf(-(expA * (av.z + dtb.z))));
-                    g4.w = lb / (1.0f + expf(-(expA * (av.w + dtb.w))));
+                    g4[i].x = lb / (1.0f + __expf(-(expA * (av.x + dtb.x))));
+                    g4[i].y = lb / (1.0f + __expf(-(expA * (av.y + dtb.y))));
+                    g4[i].z = lb / (1.0f + __expf(-(expA * (av.z + dtb.z))));
+                    g4[i].w = lb / (1.0f + __expf(-(expA * (av.w + dtb.w))));
                 } else {
-                    g4 = load4(static_cast<const float *>(a.gate) + base);
+                    g4[i] = load4(static_cast<const float *>(a.gate) + base);
                 }
             }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int t = rg + 8 * i;
             if (norm) {
-                const float qd = sqrtf(group_sum32(dot4(q4, q4)) + 1e-6f);
-                const float kd = sqrtf(group_sum32(dot4(k4, k4)) + 1e-6f);
-                q4 = make_float4(q4.x / qd, q4.y / qd, q4.z / qd, q4.w / qd);
-                k4 = make_float4(k4.x / kd, k4.y / kd, k4.z / kd, k4.w / kd);
+                const float4 k4 = make_float4(__uint_as_float(kraw[i].x << 16),
+                                              __uint_as_float(kraw[i].x & 0xffff0000u),
+                                              __uint_as_float(kraw[i].y << 16),
+                                              __uint_as_float(kraw[i].y & 0xffff0000u));
+                const float ks = group_sum32(dot4(k4, k4));
+                if (kc == 0) {
+                    sm.rnk[t] = 1.0f / sqrtf(ks + 1e-6f);
+                }
+            } else if (kc == 0) {
+                sm.rnk[t] = 1.0f;
             }
-            const float sc = a.scale;
-            float *Qr = &sm.Q[t][4 * kc];
-            Qr[0] = q4.x * sc;
-            Qr[1] = q4.y * sc;
-            Qr[2] = q4.z * sc;
-            Qr[3] = q4.w * sc;
-            float *Kr = &sm.K[t][4 * kc];
-            Kr[0] = k4.x;
-            Kr[1] = k4.y;
-            Kr[2] = k4.z;
-            Kr[3] = k4.w;
-            float *Gr = &sm.G[t][4 * kc];
-            Gr[0] = g4.x;
-            Gr[1] = g4.y;
-            Gr[2] = g4.z;
-            Gr[3] = g4.w;
-            sm.Vt[4 * kc + 0][t] = static_cast<uint16_t>(vraw.x & 0xffffu);
-            sm.Vt[4 * kc + 1][t] = static_cast<uint16_t>(vraw.x >> 16);
-            sm.Vt[4 * kc + 2][t] = static_cast<uint16_t>(vraw.y & 0xffffu);
-            sm.Vt[4 * kc + 3][t] = static_cast<uint16_t>(vraw.y >> 16);
+            *reinterpret_cast<uint2 *>(&sm.r1.K[t][4 * kc]) = kraw[i];
+            *reinterpret_cast<float4 *>(&sm.r0.G[t][4 * kc]) = g4[i];
         }
         if (tid < BT) {
             float b = 0.f;
             if (tid < len) {
                 const int64_t bi = static_cast<int64_t>(t0 + tid) * H + h;
                 if constexpr (GATE == KDA_GATE_RAW) {
-                    b = 1.0f / (1.0f + expf(-bf16_to_f32(static_cast<const uint16_t *>(a.beta)[bi])));
+                    b = 1.0f / (1.0f + __expf(-bf16_to_f32(static_cast<const uint16_t *>(a.beta)[bi])));
                 } else {
                     b = static_cast<const float *>(a.beta)[bi];
                 }
             }
             sm.beta[tid] = b;
         }
+        for (int idx = tid; idx < BT * BT; idx += kThreads) {
+            sm.LT[idx >> 6][idx & 63] = 0.f;
+        }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- S2: in-chunk cumsum of g, per channel ------------------------------
     {
@@ -332,39 +374,86 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         float run = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            run += sm.G[half * 32 + i][ch];
+            run += sm.r0.G[half * 32 + i][ch];
             vals[i] = run;
         }
         if (half == 0) {
             sm.carry[ch] = run;
         }
-        __syncthreads();
+        lds_barrier();
         const float add = half ? sm.carry[ch] : 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            sm.G[half * 32 + i][ch] = vals[i] + add;
+            sm.r0.G[half * 32 + i][ch] = vals[i] + add;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---- S3: Akk (-> LDS) and Aqk (-> fragments), wave = 16-row block I ----
-    {
-        const int I = wave;
+    auto kval = [&](int t, int k) {
+        return bf16_to_f32(sm.r1.K[t][k]) * sm.rnk[t];
+    };
+
+    // ---- S3: Akk (-> L^T in LDS), Aqk and q e^G (-> fragments) --------------
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        if (ii >= nI) {
+            break;
+        }
+        const int I = I0 + ii;
         const int ri = 16 * I + r;
+        // q row: widen, norm over all 128 channels (4 lane groups), scale
+        float qv[4][8];
+        float qss = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint2 q0 = qraw[ii][s][0];
+            const uint2 q1 = qraw[ii][s][1];
+            qv[s][0] = __uint_as_float(q0.x << 16);
+            qv[s][1] = __uint_as_float(q0.x & 0xffff0000u);
+            qv[s][2] = __uint_as_float(q0.y << 16);
+            qv[s][3] = __uint_as_float(q0.y & 0xffff0000u);
+            qv[s][4] = __uint_as_float(q1.x << 16);
+            qv[s][5] = __uint_as_float(q1.x & 0xffff0000u);
+            qv[s][6] = __uint_as_float(q1.y << 16);
+            qv[s][7] = __uint_as_float(q1.y & 0xffff0000u);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                qss += qv[s][e] * qv[s][e];
+            }
+        }
+        float qscale = a.scale;
+        if (norm) {
+            qss += __shfl_xor(qss, 16);
+            qss += __shfl_xor(qss, 32);
+            qscale = a.scale / sqrtf(qss + 1e-6f);
+        }
         bf16x8 Rh[4], Qh[4], Ql[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            float rv[8], qv[8];
+            float rv[8], qa[8], qg[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int k = 32 * s + kperm(gq, e);
-                const float ex = expf(sm.G[ri][k] - sm.G[16 * I][k]);
-                rv[e] = sm.K[ri][k] * ex;
-                qv[e] = sm.Q[ri][k] * ex;
+                const float Gi = sm.r0.G[ri][k];
+                const float ex = __expf(Gi - sm.r0.G[16 * I][k]);
+                const float qn = qv[s][e] * qscale;
+                rv[e] = kval(ri, k) * ex;
+                qa[e] = qn * ex;
+                qg[e] = qn * __expf(Gi);
             }
             Rh[s] = to_bf16x8(rv);
-            split_bf16x8(qv, Qh[s], Ql[s]);
+            split_bf16x8(qa, Qh[s], Ql[s]);
+            // q e^G fragment (mt = I, s); for I = 3 only wave 2 writes it
+            if (!(I == 3 && wave == 3)) {
+                bf16x8 fh, fl;
+                split_bf16x8(qg, fh, fl);
+                store_frag(rec, kOffQgH, I * 4 + s, lane, fh);
+                store_frag(rec, kOffQgL, I * 4 + s, lane, fl);
+            }
         }
+        // this wave's column blocks J of row block I
+        const int J0 = wave == 3 ? 2 : 0;
+        const int J1 = wave == 2 ? 1 : I;
         float aq[4][4];
 #pragma unroll
         for (int J = 0; J < 4; ++J) {
@@ -372,42 +461,56 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             for (int e = 0; e < 4; ++e) {
                 aq[J][e] = 0.f;
             }
-            if (J > I) {
+        }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    sm.L[16 * I + 4 * gq + e][16 * J + r] = 0.f;
-                }
+        for (int J = 0; J < 4; ++J) {
+            if (J < J0 || J > J1) {
                 continue;
             }
             const int rj = 16 * J + r;
-            f32x4 akk = {0.f, 0.f, 0.f, 0.f};
-            f32x4 aqt = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 akk2[2] = {z4, z4};
+            f32x4 aq3[3] = {z4, z4, z4};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 float cv[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int k = 32 * s + kperm(gq, e);
-                    cv[e] = sm.K[rj][k] * expf(sm.G[16 * I][k] - sm.G[rj][k]);
+                    cv[e] = kval(rj, k) * __expf(sm.r0.G[16 * I][k] - sm.r0.G[rj][k]);
                 }
                 bf16x8 Ch, Cl;
                 split_bf16x8(cv, Ch, Cl);
-                akk = mfma(Rh[s], Ch, akk);  // Akk[i][j]: rows i of block I
-                aqt = mfma(Ch, Qh[s], aqt);  // Aqk^T[j][i]
-                aqt = mfma(Ch, Ql[s], aqt);
-                aqt = mfma(Cl, Qh[s], aqt);
+                akk2[s & 1] = mfma(Rh[s], Ch, akk2[s & 1]);  // Akk[i][j], rows i of block I
+                aq3[0] = mfma(Ch, Qh[s], aq3[0]);            // Aqk^T[j][i]
+                aq3[1] = mfma(Ch, Ql[s], aq3[1]);
+                aq3[2] = mfma(Cl, Qh[s], aq3[2]);
             }
+            f32x4 akk, aqt;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                akk[e] = akk2[0][e] + akk2[1][e];
+                aqt[e] = (aq3[0][e] + aq3[1][e]) + aq3[2][e];
+            }
+            float4 lt;
+            float *ltp = &lt.x;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int i = 16 * I + 4 * gq + e;
                 const int j = 16 * J + r;
-                sm.L[i][j] = j < i ? akk[e] * sm.beta[i] : 0.f;
+                ltp[e] = j < i ? akk[e] * sm.beta[i] : 0.f;
                 // aqt holds Aqk[16I + r][16J + 4gq + e]
                 aq[J][e] = (16 * J + 4 * gq + e) <= ri ? aqt[e] : 0.f;
             }
+            *reinterpret_cast<float4 *>(&sm.LT[16 * J + r][16 * I + 4 * gq]) = lt;
         }
+        // Aqk fragments (mt = I, s): s covers column blocks 2s and 2s+1
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
+            const bool mine = (2 * s >= J0 && 2 * s <= (J1 | 1)) || (I < 3 && s * 2 > I);
+            if (!mine) {
+                continue;
+            }
             float x[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -420,127 +523,135 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             store_frag(rec, kOffAqL, I * 2 + s, lane, fl);
         }
     }
-    __syncthreads();
 
-    // ---- S4: q e^G, kd^T, e^(G_last), tracking operands ---------------------
-    {
-        // q e^G: fragments (mt = wave, s)
+    // ---- S4: kd^T fragments, e^(G_last), tracking operands, (e^G k)^T -------
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int t = 16 * wave + r;
+    for (int tt = 0; tt < 2; ++tt) {
+        const int mk = 2 * wave + tt;
+        const int k = 16 * mk + r;
+        const float gl = sm.r0.G[BT - 1][k];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
             float x[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int k = 32 * s + kperm(gq, e);
-                x[e] = sm.Q[t][k] * expf(sm.G[t][k]);
+                const int t = 32 * s + kperm(gq, e);
+                x[e] = kval(t, k) * __expf(gl - sm.r0.G[t][k]);
             }
             bf16x8 fh, fl;
             split_bf16x8(x, fh, fl);
-            store_frag(rec, kOffQgH, wave * 4 + s, lane, fh);
-            store_frag(rec, kOffQgL, wave * 4 + s, lane, fl);
+            store_frag(rec, kOffKdH, mk * 2 + s, lane, fh);
+            store_frag(rec, kOffKdL, mk * 2 + s, lane, fl);
         }
-        // kd^T[k][t] = k_t e^(G_last - G_t): fragments (mk = 2*wave + tt, s)
+    }
+    if (tid < DK) {
+        reinterpret_cast<float *>(rec + kOffGl)[tid] = __expf(sm.r0.G[BT - 1][tid]);
+    }
+    // The tracked prefix inside this chunk (0 < rr < len): its state is
+    // e^(G_{rr-1}) S + (e^(G_{rr-1} - G_t) k_t)_{t<rr}^T vnew.
+    if (a.track_indices != nullptr) {
+        const int ts = a.track_indices[n];
+        const int tl = a.track_lens[n];
+        const int rr = tl - BT * jc;
+        if (ts > 0 && static_cast<int64_t>(ts) < a.num_slots && rr > 0 && rr < len) {
+            char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int mk = 2 * wave + tt;
-            const int k = 16 * mk + r;
-            const float gl = sm.G[BT - 1][k];
+            for (int tt = 0; tt < 2; ++tt) {
+                const int mk = 2 * wave + tt;
+                const int k = 16 * mk + r;
+                const float gr = sm.r0.G[rr - 1][k];
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                float x[8];
+                for (int s = 0; s < 2; ++s) {
+                    float x[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int t = 32 * s + kperm(gq, e);
-                    x[e] = sm.K[t][k] * expf(gl - sm.G[t][k]);
-                }
-                bf16x8 fh, fl;
-                split_bf16x8(x, fh, fl);
-                store_frag(rec, kOffKdH, mk * 2 + s, lane, fh);
-                store_frag(rec, kOffKdL, mk * 2 + s, lane, fl);
-            }
-        }
-        if (tid < DK) {
-            reinterpret_cast<float *>(rec + kOffGl)[tid] = expf(sm.G[BT - 1][tid]);
-        }
-        // The tracked prefix inside this chunk (0 < rr < len): its state is
-        // e^(G_{rr-1}) S + (e^(G_{rr-1} - G_t) k_t)_{t<rr}^T vnew.
-        if (a.track_indices != nullptr) {
-            const int ts = a.track_indices[n];
-            const int tl = a.track_lens[n];
-            const int rr = tl - BT * jc;
-            if (ts > 0 && static_cast<int64_t>(ts) < a.num_slots && rr > 0 && rr < len) {
-                char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
-#pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    const int mk = 2 * wave + tt;
-                    const int k = 16 * mk + r;
-                    const float gr = sm.G[rr - 1][k];
-#pragma unroll
-                    for (int s = 0; s < 2; ++s) {
-                        float x[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const int t = 32 * s + kperm(gq, e);
-                            x[e] = t < rr ? sm.K[t][k] * expf(gr - sm.G[t][k]) : 0.f;
-                        }
-                        bf16x8 fh, fl;
-                        split_bf16x8(x, fh, fl);
-                        store_frag(tr, kTrOffKdH, mk * 2 + s, lane, fh);
-                        store_frag(tr, kTrOffKdL, mk * 2 + s, lane, fl);
+                    for (int e = 0; e < 8; ++e) {
+                        const int t = 32 * s + kperm(gq, e);
+                        x[e] = t < rr ? kval(t, k) * __expf(gr - sm.r0.G[t][k]) : 0.f;
                     }
+                    bf16x8 fh, fl;
+                    split_bf16x8(x, fh, fl);
+                    store_frag(tr, kTrOffKdH, mk * 2 + s, lane, fh);
+                    store_frag(tr, kTrOffKdL, mk * 2 + s, lane, fl);
                 }
-                if (tid < DK) {
-                    reinterpret_cast<float *>(tr + kTrOffGl)[tid] = expf(sm.G[rr - 1][tid]);
-                }
+            }
+            if (tid < DK) {
+                reinterpret_cast<float *>(tr + kTrOffGl)[tid] = __expf(sm.r0.G[rr - 1][tid]);
             }
         }
     }
-    __syncthreads();
-    // e^G k as bf16, transposed [k][t], over the q tile (no longer needed).
-    uint16_t(*KE)[kPadV] = reinterpret_cast<uint16_t(*)[kPadV]>(&sm.Q[0][0]);
+    uint32_t kep[16];
     {
         const int k = tid & 127;
         const int half = tid >> 7;
-#pragma unroll 8
-        for (int i = 0; i < 32; ++i) {
-            const int t = half * 32 + i;
-            KE[k][t] = f32_to_bf16(sm.K[t][k] * expf(sm.G[t][k]));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int t = half * 32 + 2 * i;
+            const uint16_t e0 = f32_to_bf16(kval(t, k) * __expf(sm.r0.G[t][k]));
+            const uint16_t e1 = f32_to_bf16(kval(t + 1, k) * __expf(sm.r0.G[t + 1][k]));
+            kep[i] = pack2(e0, e1);
         }
     }
-
-    // ---- S5: X = (I + L)^-1 (blocked, fp32), then T = X diag(beta) ----------
+    lds_barrier();  // G and K are dead from here on
     {
-        // upper blocks of X are zero; diagonal blocks by forward substitution
+        const int k = tid & 127;
+        const int half = tid >> 7;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            *reinterpret_cast<uint32_t *>(&sm.r1.KE[swz(k, half * 32 + 2 * i)]) = kep[i];
+        }
+        // v^T (bf16, swizzled), rows zero-padded
+        const int kc = tid & 31;
+        const int rg = tid >> 5;
+        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int t = rg + 8 * i;
+            uint2 vr = make_uint2(0u, 0u);
+            if (t < len) {
+                vr = *reinterpret_cast<const uint2 *>(vp + (static_cast<int64_t>(t0 + t) * H + h) * DK + 4 * kc);
+            }
+            sm.r0.late.Vt[swz(4 * kc + 0, t)] = static_cast<uint16_t>(vr.x & 0xffffu);
+            sm.r0.late.Vt[swz(4 * kc + 1, t)] = static_cast<uint16_t>(vr.x >> 16);
+            sm.r0.late.Vt[swz(4 * kc + 2, t)] = static_cast<uint16_t>(vr.y & 0xffffu);
+            sm.r0.late.Vt[swz(4 * kc + 3, t)] = static_cast<uint16_t>(vr.y >> 16);
+        }
+        // X: upper blocks zero
         for (int idx = tid; idx < BT * BT; idx += kThreads) {
             const int i = idx >> 6;
             const int j = idx & 63;
             if ((j >> 4) > (i >> 4)) {
-                sm.X[i][j] = 0.f;
-            }
-        }
-        if (lane < 16) {
-            const int b0 = 16 * wave;
-            const int col = lane;
-            float x[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float acc = i == col ? 1.f : 0.f;
-#pragma unroll
-                for (int jj = 0; jj < i; ++jj) {
-                    acc -= sm.L[b0 + i][b0 + jj] * x[jj];
-                }
-                x[i] = acc;
-            }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                sm.X[b0 + i][b0 + col] = x[i];
+                sm.r0.late.X[i][j] = 0.f;
             }
         }
     }
-    __syncthreads();
+
+    // ---- S5: X = (I + L)^-1 (blocked, fp32), then T = X diag(beta) ----------
+    // Diagonal 16x16 blocks, right-looking: column c of block w per lane c.
+    if (lane < 16) {
+        const int b0 = 16 * wave;
+        const int col = lane;
+        float acc[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            acc[i] = i == col ? 1.f : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 15; ++j) {
+            const float xj = acc[j];
+#pragma unroll
+            for (int i = j + 1; i < 16; ++i) {
+                acc[i] -= sm.LT[b0 + j][b0 + i] * xj;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            sm.r0.late.X[b0 + i][b0 + col] = acc[i];
+        }
+    }
+    lds_barrier();
     // Off-diagonal blocks by level d = I - J:
-    //   M_IJ = sum_{K=J}^{I-1} L_IK X_KJ,  X_IJ = -X_II M_IJ.
-    // M_IJ is parked in the (still zero) upper block (J, I) of X.
+    //   M_IJ = sum_{K=J}^{I-1} L_IK X_KJ,  X_IJ = -X_II M_IJ;
+    // M_IJ is parked (transposed) in the still-zero upper block (J, I).
     for (int d = 1; d < 4; ++d) {
         const int nb = 4 - d;
         for (int idx = tid; idx < nb * 256; idx += kThreads) {
@@ -549,12 +660,13 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             const int i = (idx >> 4) & 15;
             const int jj = idx & 15;
             float acc = 0.f;
+#pragma unroll 16
             for (int kk = 16 * J; kk < 16 * I; ++kk) {
-                acc += sm.L[16 * I + i][kk] * sm.X[kk][16 * J + jj];
+                acc += sm.LT[kk][16 * I + i] * sm.r0.late.X[kk][16 * J + jj];
             }
-            sm.X[16 * J + jj][16 * I + i] = acc;  // M_IJ[i][jj], transposed into (J, I)
+            sm.r0.late.X[16 * J + jj][16 * I + i] = acc;
         }
-        __syncthreads();
+        lds_barrier();
         for (int idx = tid; idx < nb * 256; idx += kThreads) {
             const int J = idx >> 8;
             const int I = J + d;
@@ -563,26 +675,26 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             float acc = 0.f;
 #pragma unroll
             for (int kk = 0; kk < 16; ++kk) {
-                acc += sm.X[16 * I + i][16 * I + kk] * sm.X[16 * J + jj][16 * I + kk];
+                acc += sm.r0.late.X[16 * I + i][16 * I + kk] * sm.r0.late.X[16 * J + jj][16 * I + kk];
             }
-            sm.X[16 * I + i][16 * J + jj] = -acc;
+            sm.r0.late.X[16 * I + i][16 * J + jj] = -acc;
         }
-        __syncthreads();
+        lds_barrier();
         for (int idx = tid; idx < nb * 256; idx += kThreads) {
             const int J = idx >> 8;
             const int I = J + d;
             const int i = (idx >> 4) & 15;
             const int jj = idx & 15;
-            sm.X[16 * J + jj][16 * I + i] = 0.f;
+            sm.r0.late.X[16 * J + jj][16 * I + i] = 0.f;
         }
-        __syncthreads();
+        lds_barrier();
     }
     for (int idx = tid; idx < BT * BT; idx += kThreads) {
         const int i = idx >> 6;
         const int j = idx & 63;
-        sm.X[i][j] *= sm.beta[j];
+        sm.r0.late.X[i][j] *= sm.beta[j];
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- S6: u = T v (T split) and w^T = (e^G k)^T T^T (single) --------------
     {
@@ -591,25 +703,30 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         bf16x8 Th[2], Tl[2];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            float x[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                x[e] = sm.X[t][32 * s + kperm(gq, e)];
-            }
+            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.r0.late.X[t][32 * s + 4 * gq]);
+            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.r0.late.X[t][32 * s + 16 + 4 * gq]);
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             split_bf16x8(x, Th[s], Tl[s]);
         }
         // u tiles (mt = wave, vt): A = T rows, B = v (K = j)
+#pragma unroll 2
         for (int vt = 0; vt < 8; ++vt) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc[2] = {z4, z4};
             for (int s = 0; s < nS; ++s) {
-                const uint16_t *vr = &sm.Vt[16 * vt + r][32 * s];
-                const uint2 v0 = *reinterpret_cast<const uint2 *>(vr + 4 * gq);
-                const uint2 v1 = *reinterpret_cast<const uint2 *>(vr + 16 + 4 * gq);
+                const int row = 16 * vt + r;
+                const uint2 v0 = *reinterpret_cast<const uint2 *>(&sm.r0.late.Vt[swz(row, 32 * s + 4 * gq)]);
+                const uint2 v1 = *reinterpret_cast<const uint2 *>(&sm.r0.late.Vt[swz(row, 32 * s + 16 + 4 * gq)]);
                 const bf16x8 vb = as_bf16x8(u32x4{v0.x, v0.y, v1.x, v1.y});
-                acc = mfma(Th[s], vb, acc);
-                acc = mfma(Tl[s], vb, acc);
+                acc[0] = mfma(Th[s], vb, acc[0]);
+                acc[1] = mfma(Tl[s], vb, acc[1]);
             }
-            reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = acc;
+            f32x4 uo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uo[i] = acc[0][i] + acc[1][i];
+            }
+            reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = uo;
         }
         // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k, B = T^T (K = j)
         for (int sp = 0; sp < 4; ++sp) {
@@ -619,9 +736,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 const int mk = 2 * sp + half;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
                 for (int s = 0; s < nS; ++s) {
-                    const uint16_t *kr = &KE[16 * mk + r][32 * s];
-                    const uint2 k0 = *reinterpret_cast<const uint2 *>(kr + 4 * gq);
-                    const uint2 k1 = *reinterpret_cast<const uint2 *>(kr + 16 + 4 * gq);
+                    const int row = 16 * mk + r;
+                    const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.r1.KE[swz(row, 32 * s + 4 * gq)]);
+                    const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.r1.KE[swz(row, 32 * s + 16 + 4 * gq)]);
                     const bf16x8 kb = as_bf16x8(u32x4{k0.x, k0.y, k1.x, k1.y});
                     acc = mfma(kb, Th[s], acc);
                 }
@@ -643,6 +760,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws) {
     __shared__ u32x4 sfrag[4][2][64];     // S as B fragments, slice s = k rows [32s, 32s+32)
     __shared__ uint32_t vfrag[2][2][64][4];  // vnew as B fragments, slice s = tokens [32s, 32s+32)
+    __shared__ uint32_t otile[4][16][8];     // per wave: its 16 output rows x 16 bf16 columns
 
     const int H = a.num_heads;
     const int N = a.num_seqs;
@@ -717,35 +835,40 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs
     uint16_t *out = static_cast<uint16_t *>(a.out);
     const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
 
-    for (int j = 0; j < nch; ++j) {
-        const char *rec = ws + LY.recs + (static_cast<size_t>(c0 + j) * H + h) * kRecBytes;
-        const int t0 = bos + BT * j;
-        const int len = eos - t0 < BT ? eos - t0 : BT;
-
-        // operands of this chunk
+    // One chunk's operands, held in registers. Two sets alternate so the
+    // next chunk's fragments are in flight while this chunk computes.
+    struct Ops {
         bf16x8 Wf[4], Qh[4], Ql[4], Ah[2], Al[2], Kh[2][2], Kl[2][2];
+        f32x4 u, gl[2];
+    };
+    auto load_ops = [&](Ops &op, int j) {
+        const char *rec = ws + LY.recs + (static_cast<size_t>(c0 + j) * H + h) * kRecBytes;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            Wf[s] = load_frag(rec, kOffW, w * 4 + s, lane);
-            Qh[s] = load_frag(rec, kOffQgH, w * 4 + s, lane);
-            Ql[s] = load_frag(rec, kOffQgL, w * 4 + s, lane);
+            op.Wf[s] = load_frag(rec, kOffW, w * 4 + s, lane);
+            op.Qh[s] = load_frag(rec, kOffQgH, w * 4 + s, lane);
+            op.Ql[s] = load_frag(rec, kOffQgL, w * 4 + s, lane);
         }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            Ah[s] = load_frag(rec, kOffAqH, w * 2 + s, lane);
-            Al[s] = load_frag(rec, kOffAqL, w * 2 + s, lane);
+            op.Ah[s] = load_frag(rec, kOffAqH, w * 2 + s, lane);
+            op.Al[s] = load_frag(rec, kOffAqL, w * 2 + s, lane);
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                Kh[tt][s] = load_frag(rec, kOffKdH, (2 * w + tt) * 2 + s, lane);
-                Kl[tt][s] = load_frag(rec, kOffKdL, (2 * w + tt) * 2 + s, lane);
+                op.Kh[tt][s] = load_frag(rec, kOffKdH, (2 * w + tt) * 2 + s, lane);
+                op.Kl[tt][s] = load_frag(rec, kOffKdL, (2 * w + tt) * 2 + s, lane);
             }
         }
-        const f32x4 u = reinterpret_cast<const f32x4 *>(rec + kOffU)[(w * 8 + vt) * 64 + lane];
-        f32x4 gl[2];
+        op.u = reinterpret_cast<const f32x4 *>(rec + kOffU)[(w * 8 + vt) * 64 + lane];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            gl[tt] = *reinterpret_cast<const f32x4 *>(rec + kOffGl + 4 * (16 * (2 * w + tt) + 4 * gq));
+            op.gl[tt] = *reinterpret_cast<const f32x4 *>(rec + kOffGl + 4 * (16 * (2 * w + tt) + 4 * gq));
         }
+    };
+
+    auto step = [&](const Ops &op, int j) {
+        const int t0 = bos + BT * j;
+        const int len = eos - t0 < BT ? eos - t0 : BT;
 
         // 1. publish S (slice s = w) as hi/lo B fragments
         {
@@ -760,36 +883,37 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs
             sfrag[w][0][lane] = as_u32x4(hi);
             sfrag[w][1][lane] = as_u32x4(lo);
         }
-        __syncthreads();
+        lds_barrier();
 
-        // 2. vnew rows [16w, 16w+16) = u - w S ; 3. o = (q e^G) S (3-pass)
-        f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f};
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        // 2. vnew rows [16w, 16w+16) = u - w S ; 3. o = (q e^G) S (3-pass).
+        // Independent accumulators (per pass, per slice parity) keep several
+        // MFMA chains in flight: with one wave per SIMD a single dependent
+        // chain would pay the full MFMA latency on every link.
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+        f32x4 wsa[2] = {z4, z4};
+        f32x4 oq[3] = {z4, z4, z4};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const bf16x8 sh = as_bf16x8(sfrag[s][0][lane]);
             const bf16x8 sl = as_bf16x8(sfrag[s][1][lane]);
-            ws_acc = mfma(Wf[s], sh, ws_acc);
-            o = mfma(Qh[s], sh, o);
-            o = mfma(Qh[s], sl, o);
-            o = mfma(Ql[s], sh, o);
+            wsa[s & 1] = mfma(op.Wf[s], sh, wsa[s & 1]);
+            oq[0] = mfma(op.Qh[s], sh, oq[0]);
+            oq[1] = mfma(op.Qh[s], sl, oq[1]);
+            oq[2] = mfma(op.Ql[s], sh, oq[2]);
         }
         f32x4 vn;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            vn[i] = u[i] - ws_acc[i];
+            vn[i] = op.u[i] - (wsa[0][i] + wsa[1][i]);
         }
         // 4. publish vnew (tile mt = w is half w%2 of slice w/2)
         {
             uint32_t hp[2], lp[2];
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                const uint16_t h0 = f32_to_bf16(vn[2 * p]);
-                const uint16_t h1 = f32_to_bf16(vn[2 * p + 1]);
-                const uint16_t l0 = f32_to_bf16(vn[2 * p] - bf16_to_f32(h0));
-                const uint16_t l1 = f32_to_bf16(vn[2 * p + 1] - bf16_to_f32(h1));
-                hp[p] = pack2(h0, h1);
-                lp[p] = pack2(l0, l1);
+                hp[p] = pack_bf16x2(vn[2 * p], vn[2 * p + 1]);
+                lp[p] = pack_bf16x2(vn[2 * p] - __uint_as_float(hp[p] << 16),
+                                    vn[2 * p + 1] - __uint_as_float(hp[p] & 0xffff0000u));
             }
             const int sl = w >> 1;
             const int hf = (w & 1) * 2;
@@ -798,7 +922,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs
             vfrag[sl][1][lane][hf] = lp[0];
             vfrag[sl][1][lane][hf + 1] = lp[1];
         }
-        __syncthreads();
+        lds_barrier();
 
         bf16x8 vh[2], vl[2];
 #pragma unroll
@@ -809,17 +933,38 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs
                                     vfrag[s][1][lane][3]});
         }
         // 5. o += Aqk vnew (3-pass) and store rows t < len
+        f32x4 oa[3] = {z4, z4, z4};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            o = mfma(Ah[s], vh[s], o);
-            o = mfma(Ah[s], vl[s], o);
-            o = mfma(Al[s], vh[s], o);
+            oa[0] = mfma(op.Ah[s], vh[s], oa[0]);
+            oa[1] = mfma(op.Ah[s], vl[s], oa[1]);
+            oa[2] = mfma(op.Al[s], vh[s], oa[2]);
         }
+        f32x4 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = 16 * w + 4 * gq + i;
+            o[i] = ((oq[0][i] + oq[1][i]) + oq[2][i]) + ((oa[0][i] + oa[1][i]) + oa[2][i]);
+        }
+        // Output rows [16w, 16w+16) x 16 columns: transposed through this
+        // wave's own LDS tile so each lane stores 4 consecutive columns of one
+        // row (one 8-byte nontemporal store per lane instead of four 2-byte
+        // stores; no workgroup barrier -- the tile is private to the wave).
+        {
+            uint16_t *ot = reinterpret_cast<uint16_t *>(&otile[w][0][0]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ot[(4 * gq + i) * 16 + r] = f32_to_bf16(o[i]);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            const int row = lane >> 2;
+            const int cq = lane & 3;
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 val = *reinterpret_cast<const u32x2 *>(&otile[w][row][2 * cq]);
+            const int t = 16 * w + row;
             if (t < len) {
-                out[(static_cast<int64_t>(t0 + t) * H + h) * DK + vcol] = f32_to_bf16(o[i]);
+                __builtin_nontemporal_store(
+                    val, reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(t0 + t) * H + h) * DK +
+                                                   16 * vt + 4 * cq));
             }
         }
         // tracked prefix strictly inside this chunk
@@ -834,34 +979,59 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs
                 for (int i = 0; i < 4; ++i) {
                     St[tt][i] = S[tt][i] * g2[i];
                 }
+                f32x4 tu[3] = {z4, z4, z4};
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
                     const bf16x8 th = load_frag(tr, kTrOffKdH, (2 * w + tt) * 2 + s, lane);
                     const bf16x8 tl = load_frag(tr, kTrOffKdL, (2 * w + tt) * 2 + s, lane);
-                    St[tt] = mfma(th, vh[s], St[tt]);
-                    St[tt] = mfma(th, vl[s], St[tt]);
-                    St[tt] = mfma(tl, vh[s], St[tt]);
+                    tu[0] = mfma(th, vh[s], tu[0]);
+                    tu[1] = mfma(th, vl[s], tu[1]);
+                    tu[2] = mfma(tl, vh[s], tu[2]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    St[tt][i] += (tu[0][i] + tu[1][i]) + tu[2][i];
                 }
             }
             store_S(track_slot, St);
         }
-        // 6. S <- e^(G_last) S + kd^T vnew (3-pass)
+        // 6. S <- e^(G_last) S + kd^T vnew (3-pass, independent chains)
+        f32x4 su[2][3] = {{z4, z4, z4}, {z4, z4, z4}};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                su[tt][0] = mfma(op.Kh[tt][s], vh[s], su[tt][0]);
+                su[tt][1] = mfma(op.Kh[tt][s], vl[s], su[tt][1]);
+                su[tt][2] = mfma(op.Kl[tt][s], vh[s], su[tt][2]);
+            }
+        }
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                S[tt][i] *= gl[tt][i];
-            }
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                S[tt] = mfma(Kh[tt][s], vh[s], S[tt]);
-                S[tt] = mfma(Kh[tt][s], vl[s], S[tt]);
-                S[tt] = mfma(Kl[tt][s], vh[s], S[tt]);
+                S[tt][i] = S[tt][i] * op.gl[tt][i] + ((su[tt][0][i] + su[tt][1][i]) + su[tt][2][i]);
             }
         }
         if (track_slot > 0 && rr == len) {
             store_S(track_slot, S);
         }
+    };
+
+    // The prefetches are unconditional (clamped to the last chunk) so the
+    // compiler's wait counts stay exact on every path through the loop.
+    Ops opA, opB;
+    if (nch > 0) {
+        load_ops(opA, 0);
+    }
+    for (int j = 0; j < nch; j += 2) {
+        load_ops(opB, j + 1 < nch ? j + 1 : nch - 1);
+        step(opA, j);
+        if (j + 1 >= nch) {
+            break;
+        }
+        load_ops(opA, j + 2 < nch ? j + 2 : nch - 1);
+        step(opB, j + 1);
     }
 
     // Tokens outside every sequence are written as zero.
@@ -953,8 +1123,8 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     const int nrec = max_chunks(a.num_tokens, a.num_seqs);
     {
         const void *fn = a.gate_mode == KDA_GATE_RAW
-                             ? reinterpret_cast<const void *>(chunk_prepare_kernel<uint16_t, KDA_GATE_RAW>)
-                             : reinterpret_cast<const void *>(chunk_prepare_kernel<uint16_t, KDA_GATE_LOG>);
+                             ? reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_RAW>)
+                             : reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_LOG>);
         int nr = nrec;
         void *params[] = {&kargs, &ws, &nr};
         if (hipLaunchKernel(fn, dim3(static_cast<unsigned>(nrec), static_cast<unsigned>(a.num_heads)),

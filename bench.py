@@ -181,6 +181,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workload")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode workload")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (the known-size kernel "
+                         "the FETCH_SIZE / WRITE_SIZE counters are scaled by), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
@@ -188,8 +192,24 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * 2 ** 20 // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        _log(f"copy calibration: 5 x {args.copy_calibration} MiB device copies")
+        return
     import sgl_glm53_ascend_ops  # noqa: F401
 
+    if args.no_decode:
+        # profiling aid: the prefill workload alone (no JSON line)
+        _log("prefill: config 3 (T=8192, H=32, K=V=128, chunk 64)")
+        pf = run_prefill(max(3, args.steps // 5), max(1, args.warmup // 5))
+        if pf is not None:
+            _log(f"prefill: {pf['ms_per_step']*1e3:.1f} us/step")
+        return
     _log("decode: config 2 (B=256, H=32, K=V=128)")
     dec = run_decode(args.steps, args.warmup)
     tok_s = DEC_N / (dec["ms_per_step"] / 1e3)
