@@ -392,6 +392,32 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     auto kval = [&](int t, int k) {
         return bf16_to_f32(sm.r1.K[t][k]) * sm.rnk[t];
     };
+    // 8 channels {32s + kperm(gq, e)} of one row: two 8-byte k reads, two
+    // 16-byte G reads (vector LDS accesses instead of per-element ones).
+    auto load_k8 = [&](int row, int s, float x[8]) {
+        const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.r1.K[row][32 * s + 4 * gq]);
+        const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.r1.K[row][32 * s + 16 + 4 * gq]);
+        x[0] = __uint_as_float(k0.x << 16);
+        x[1] = __uint_as_float(k0.x & 0xffff0000u);
+        x[2] = __uint_as_float(k0.y << 16);
+        x[3] = __uint_as_float(k0.y & 0xffff0000u);
+        x[4] = __uint_as_float(k1.x << 16);
+        x[5] = __uint_as_float(k1.x & 0xffff0000u);
+        x[6] = __uint_as_float(k1.y << 16);
+        x[7] = __uint_as_float(k1.y & 0xffff0000u);
+    };
+    auto load_g8 = [&](int row, int s, float x[8]) {
+        const float4 g0 = *reinterpret_cast<const float4 *>(&sm.r0.G[row][32 * s + 4 * gq]);
+        const float4 g1 = *reinterpret_cast<const float4 *>(&sm.r0.G[row][32 * s + 16 + 4 * gq]);
+        x[0] = g0.x;
+        x[1] = g0.y;
+        x[2] = g0.z;
+        x[3] = g0.w;
+        x[4] = g1.x;
+        x[5] = g1.y;
+        x[6] = g1.z;
+        x[7] = g1.w;
+    };
 
     // ---- S3: Akk (-> L^T in LDS), Aqk and q e^G (-> fragments) --------------
 #pragma unroll
@@ -427,19 +453,26 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             qss += __shfl_xor(qss, 32);
             qscale = a.scale / sqrtf(qss + 1e-6f);
         }
+        // the block's anchor row G[16I][.], kept for every column block
+        float anc[4][8];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            load_g8(16 * I, s, anc[s]);
+        }
+        const float rki = sm.rnk[ri];
         bf16x8 Rh[4], Qh[4], Ql[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            float rv[8], qa[8], qg[8];
+            float kk[8], gg[8], rv[8], qa[8], qg[8];
+            load_k8(ri, s, kk);
+            load_g8(ri, s, gg);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int k = 32 * s + kperm(gq, e);
-                const float Gi = sm.r0.G[ri][k];
-                const float ex = __expf(Gi - sm.r0.G[16 * I][k]);
+                const float ex = __expf(gg[e] - anc[s][e]);
                 const float qn = qv[s][e] * qscale;
-                rv[e] = kval(ri, k) * ex;
+                rv[e] = kk[e] * rki * ex;
                 qa[e] = qn * ex;
-                qg[e] = qn * __expf(Gi);
+                qg[e] = qn * __expf(gg[e]);
             }
             Rh[s] = to_bf16x8(rv);
             split_bf16x8(qa, Qh[s], Ql[s]);
@@ -468,16 +501,18 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 continue;
             }
             const int rj = 16 * J + r;
+            const float rkj = sm.rnk[rj];
             const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
             f32x4 akk2[2] = {z4, z4};
             f32x4 aq3[3] = {z4, z4, z4};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                float cv[8];
+                float kk[8], gg[8], cv[8];
+                load_k8(rj, s, kk);
+                load_g8(rj, s, gg);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const int k = 32 * s + kperm(gq, e);
-                    cv[e] = kval(rj, k) * __expf(sm.r0.G[16 * I][k] - sm.r0.G[rj][k]);
+                    cv[e] = kk[e] * rkj * __expf(anc[s][e] - gg[e]);
                 }
                 bf16x8 Ch, Cl;
                 split_bf16x8(cv, Ch, Cl);
@@ -630,6 +665,10 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     if (lane < 16) {
         const int b0 = 16 * wave;
         const int col = lane;
+        // Constant loop bounds with a compile-time i > j mask: every acc[]
+        // index is static, so the array stays in registers (a bound that
+        // depends on j leaves the inner loop rolled and turns acc[] into a
+        // runtime-indexed select chain).
         float acc[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -638,9 +677,20 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 #pragma unroll
         for (int j = 0; j < 15; ++j) {
             const float xj = acc[j];
+            float lrow[16];
 #pragma unroll
-            for (int i = j + 1; i < 16; ++i) {
-                acc[i] -= sm.LT[b0 + j][b0 + i] * xj;
+            for (int q = 0; q < 4; ++q) {
+                const float4 t4 = *reinterpret_cast<const float4 *>(&sm.LT[b0 + j][b0 + 4 * q]);
+                lrow[4 * q + 0] = t4.x;
+                lrow[4 * q + 1] = t4.y;
+                lrow[4 * q + 2] = t4.z;
+                lrow[4 * q + 3] = t4.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (i > j) {
+                    acc[i] -= lrow[i] * xj;
+                }
             }
         }
 #pragma unroll
@@ -709,11 +759,15 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             split_bf16x8(x, Th[s], Tl[s]);
         }
         // u tiles (mt = wave, vt): A = T rows, B = v (K = j)
-#pragma unroll 2
+#pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
             const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
             f32x4 acc[2] = {z4, z4};
-            for (int s = 0; s < nS; ++s) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                if (s >= nS) {
+                    break;  // uniform per wave; keeps s (and Th[s]) static
+                }
                 const int row = 16 * vt + r;
                 const uint2 v0 = *reinterpret_cast<const uint2 *>(&sm.r0.late.Vt[swz(row, 32 * s + 4 * gq)]);
                 const uint2 v1 = *reinterpret_cast<const uint2 *>(&sm.r0.late.Vt[swz(row, 32 * s + 16 + 4 * gq)]);
@@ -735,7 +789,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             for (int half = 0; half < 2; ++half) {
                 const int mk = 2 * sp + half;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                for (int s = 0; s < nS; ++s) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    if (s >= nS) {
+                        break;
+                    }
                     const int row = 16 * mk + r;
                     const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.r1.KE[swz(row, 32 * s + 4 * gq)]);
                     const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.r1.KE[swz(row, 32 * s + 16 + 4 * gq)]);
