@@ -45,6 +45,19 @@ BYTES_PER_TOKEN_HEAD = 2 * DEC_D * DEC_D * 4 + 3 * DEC_D * 2 + DEC_D * 4 + 4 + D
 # + cu_seqlens (257 x 4) + indices (256 x 4) + ... as quoted: 2052 B of metadata.
 DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
 
+# HBM bytes per decode launch, from two rocprofv3 --pmc passes over
+# ``bench.py --no-cpu --no-prefill`` (FETCH_SIZE, then WRITE_SIZE, KiB per
+# dispatch), each scaled by what the same counter reads for a 512 MiB device
+# copy (``--copy-calibration 512``): FETCH_SIZE reads 262156.8 KiB for the
+# copy's 524288 KiB of reads (scale 2.0), WRITE_SIZE reads 524288 KiB (1.0).
+# The kernel-trace/PMC summaries are kept under profiles/.
+FETCH_SCALE = 524288.0 / 262156.8
+WRITE_SCALE = 524288.0 / 524288.0
+DEC_FETCH_KIB, DEC_WRITE_KIB = 271558.7, 526401.0
+DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
+# Same for the two prefill kernels (prepare K1, scan K2) on config 3.
+PF_TRAFFIC = ((180848.0 + 264263.9) * FETCH_SCALE + (526336.0 + 108322.7) * WRITE_SCALE) * 1024
+
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
 # Dense-tile FLOPs per token-head: 2*(5*BT*D + 3*D*D).
@@ -231,6 +244,7 @@ def main():
                 tflops=tf,
                 mfma_frac=tf / BF16_PEAK_TFLOPS,
                 hbm_gbs=PF_BYTES / (pf["gpu_us"] * 1e-6) / 1e9,
+                traffic=PF_TRAFFIC,
                 attainable_frac=(tf * 1e12) / min(BF16_PEAK_TFLOPS * 1e12,
                                                   HBM_PEAK_GBS * 1e9 * PF_FLOP / PF_BYTES),
             )
@@ -264,7 +278,7 @@ def main():
         state_hbm_gbs=achieved,
         roofline=dict(
             bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
-            frac=achieved / HBM_PEAK_GBS, traffic=None,
+            frac=achieved / HBM_PEAK_GBS, traffic=DEC_TRAFFIC,
             kernel="recurrent_kernel<128,8,bf16,bf16,LOG>",
             algorithmic_bytes_per_launch=DEC_BYTES, kernel_us=dec["kernel_us"],
         ),
