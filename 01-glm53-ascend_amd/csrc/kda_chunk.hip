@@ -23,9 +23,10 @@
 //                           fp32, w and u on MFMA; writes the scan's operands as
 //                           ready MFMA fragments;
 //   K2 chunk_scan_kernel    one workgroup per (sequence, head, 16 value
-//                           columns), the serial chunk recurrence: four waves
-//                           split the rows of each product and exchange S and
-//                           vnew through LDS; S stays fp32 in registers.
+//                           columns), the serial chunk recurrence: four chain
+//                           waves carry S (fp32, registers) and vnew, four
+//                           output waves compute o one phase behind; S and
+//                           vnew are exchanged through LDS.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16 with fp32 accumulation. Operands whose
 // rounding would break the tolerance contract are carried as bf16 hi + lo
@@ -201,35 +202,56 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
 // ---------------------------------------------------------------------------
 // K1: per (chunk, head) intra-chunk work.
 //
-// 68 KiB of LDS, so two workgroups share a CU and one's loads overlap the
-// other's math. k is kept as its bf16 input plus a per-row inverse norm, q
-// never enters LDS (each wave loads its own rows into registers), and the
-// solve's X and v^T reuse the cumsum tile once it is dead.
+// About 71 KiB of LDS, so two workgroups share a CU and one's loads overlap
+// the other's math. Every global load of the chunk (k, g, beta, v and each
+// wave's q rows) is issued up front. k stays as its bf16 input plus a per-row
+// inverse norm; the decay is accumulated in log2 units, so each exponential is
+// one v_exp_f32. v and e^G k stay row-major and are read as MFMA operands with
+// gfx950's transposing LDS read ds_read_b64_tr_b16: within each group of 16
+// lanes, lane 16G + i receives as element m the (i % 4)-th 16-bit value of the
+// 8-byte word addressed by lane 16G + 4m + i / 4. The solve's X and the v tile
+// reuse the cumsum tile once it is dead.
 // ---------------------------------------------------------------------------
 
-constexpr int kPadF = 132;  // fp32 row stride of [64][128] tiles (bank spread)
-constexpr int kPadK = 136;  // bf16 row stride of the k tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kPadF = 132;  // fp32 row stride of [64][128] tiles (16-lane float4 reads)
+constexpr int kPadK = 136;  // bf16 row stride of the k tile (32-lane 8-byte reads)
+constexpr int kPadT = 144;  // bf16 row stride of tiles read transposed
 constexpr int kPadX = 68;   // fp32 row stride of [64][64] tiles (16-B rows)
 
-// [128][64] bf16 tiles stored with 8-element groups XOR-swizzled by the row,
-// so the 16 rows a wave reads at one column land in different banks.
-__device__ __forceinline__ int swz(int row, int col) {
-    return row * 64 + ((((col >> 3) ^ (row & 7)) << 3) | (col & 7));
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// MFMA operand from a row-major bf16 LDS tile whose rows are the K index:
+// lane (r, g) receives tile[row0 + kperm(g, e)][col0 + r], e = 0..7 (two
+// transposing reads, rows row0 + 4g + m and row0 + 16 + 4g + m).
+__device__ __forceinline__ bf16x8 lds_tr_frag(const uint16_t *tile, int row0, int col0, int lane) {
+    const int g = lane >> 4;
+    const int m = (lane >> 2) & 3;
+    const int c4 = lane & 3;
+    const uint16_t *p0 = tile + (row0 + 4 * g + m) * kPadT + col0 + 4 * c4;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0 + 16 * kPadT));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 struct PrepShared {
     union {
-        float G[BT][kPadF];  // cumsum of the log decay (S1-S4)
+        float G[BT][kPadF];  // cumsum of the log2 decay (S1-S4)
         struct {
-            float X[BT][kPadX];       // (I + L)^-1, then T = X diag(beta) (S5-S6)
-            uint16_t Vt[DK * BT];     // v^T, bf16 bits, swizzled (S5-S6)
+            float X[BT][kPadX];     // (I + L)^-1, then T = X diag(beta) (S5-S6)
+            uint16_t V[BT][kPadT];  // v, bf16 bits, row-major (S5-S6)
         } late;
     } r0;
     union {
         uint16_t K[BT][kPadK];   // k, bf16 input bits (S1-S4)
-        uint16_t KE[DK * BT];    // (e^G k)^T as bf16, swizzled (S4-S6)
+        uint16_t KE[BT][kPadT];  // e^G k as bf16, row-major (S4-S6)
     } r1;
-    float LT[BT][kPadX];  // L^T: LT[j][i] = beta_i Akk[i][j] (j < i)
+    // Strict upper triangle: L^T, LT[j][i] = beta_i Akk[i][j] (j < i).
+    // Lower triangle with the diagonal: Aqk[i][j] (j <= i).
+    float LT[BT][kPadX];
     float beta[BT];
     float rnk[BT];        // k row scale (1 / norm, or 1)
     float carry[DK];
@@ -274,34 +296,40 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     const bool norm = GATE == KDA_GATE_RAW || a.qk_l2norm != 0;
     const uint16_t *qp = static_cast<const uint16_t *>(a.q);
 
-    // Row blocks I this wave builds Akk/Aqk pairs for (balanced over waves):
-    //   wave 0: (0,0) (1,0) (1,1)   wave 1: (2,0) (2,1) (2,2)
-    //   wave 2: (3,0) (3,1)         wave 3: (3,2) (3,3)
-    const int nI = wave == 0 ? 2 : 1;
-    const int I0 = wave == 0 ? 0 : (wave == 1 ? 2 : 3);
-    // Its q rows, loaded now so the loads overlap S1/S2: lane (r, gq) holds
-    // q[16I + r][32s + kperm(gq, e)] as 4 x (4 bf16) per slice pair.
+    // S3 work units: (row block I, channel half sh = slices 2sh and 2sh+1),
+    // each with its pairs (I, J <= I); the two halves of every product meet
+    // in LDS through float atomics. Five half-pairs and two half-blocks per
+    // wave:  wave 0: (3,0) (0,0)   wave 1: (3,1) (0,1)
+    //        wave 2: (2,0) (1,0)   wave 3: (2,1) (1,1)
+    const int sh = wave & 1;
+    const int IA = wave < 2 ? 3 : 2;
+    // q rows of both blocks, loaded now so the loads overlap S1/S2: lane (r, gq)
+    // holds q[16I + r][32s + kperm(gq, e)] as 2 x (4 bf16) per slice; entries
+    // 0, 1 are this wave's slices, 2, 3 the other half's (read for the norm).
     uint2 qraw[2][4][2];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
-        const int t = 16 * (I0 + ii) + r;
+        const int t = 16 * (ii == 0 ? IA : 3 - IA) + r;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            qraw[ii][s][0] = make_uint2(0u, 0u);
-            qraw[ii][s][1] = make_uint2(0u, 0u);
-            if (ii < nI && t < len) {
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int s = q4 < 2 ? 2 * sh + q4 : 2 * (1 - sh) + (q4 - 2);
+            qraw[ii][q4][0] = make_uint2(0u, 0u);
+            qraw[ii][q4][1] = make_uint2(0u, 0u);
+            if (t < len && (q4 < 2 || norm)) {
                 const uint16_t *row = qp + (static_cast<int64_t>(t0 + t) * H + h) * DK + 32 * s;
-                qraw[ii][s][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
-                qraw[ii][s][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
+                qraw[ii][q4][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
+                qraw[ii][q4][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
             }
         }
     }
 
-    // ---- S1: k rows, log decay, beta (zero-padded); L^T cleared -------------
+    // ---- S1: k rows, log2 decay, beta, v (zero-padded) ---------------------
+    const int kc = tid & 31;
+    const int rg = tid >> 5;
+    uint2 vraw[8];  // v rows rg + 8i, columns 4kc..4kc+3 (written to LDS after S4)
     {
-        const int kc = tid & 31;
-        const int rg = tid >> 5;
         const uint16_t *kp = static_cast<const uint16_t *>(a.k);
+        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
         float expA = 0.f;
         float4 dtb = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (GATE == KDA_GATE_RAW) {
@@ -315,9 +343,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             const int t = rg + 8 * i;
             const int64_t base = (static_cast<int64_t>(t0 + t) * H + h) * DK + 4 * kc;
             kraw[i] = make_uint2(0u, 0u);
+            vraw[i] = make_uint2(0u, 0u);
             g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (t < len) {
                 kraw[i] = *reinterpret_cast<const uint2 *>(kp + base);
+                vraw[i] = *reinterpret_cast<const uint2 *>(vp + base);
                 if constexpr (GATE == KDA_GATE_RAW) {
                     const float4 av = load4(static_cast<const uint16_t *>(a.gate) + base);
                     const float lb = a.lower_bound;
@@ -346,7 +376,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 sm.rnk[t] = 1.0f;
             }
             *reinterpret_cast<uint2 *>(&sm.r1.K[t][4 * kc]) = kraw[i];
-            *reinterpret_cast<float4 *>(&sm.r0.G[t][4 * kc]) = g4[i];
+            *reinterpret_cast<float4 *>(&sm.r0.G[t][4 * kc]) =
+                make_float4(g4[i].x * kLog2e, g4[i].y * kLog2e, g4[i].z * kLog2e, g4[i].w * kLog2e);
         }
         if (tid < BT) {
             float b = 0.f;
@@ -360,13 +391,10 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             }
             sm.beta[tid] = b;
         }
-        for (int idx = tid; idx < BT * BT; idx += kThreads) {
-            sm.LT[idx >> 6][idx & 63] = 0.f;
-        }
     }
     lds_barrier();
 
-    // ---- S2: in-chunk cumsum of g, per channel ------------------------------
+    // ---- S2: in-chunk cumsum of the log2 decay, per channel -----------------
     {
         const int ch = tid & 127;
         const int half = tid >> 7;
@@ -393,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         return bf16_to_f32(sm.r1.K[t][k]) * sm.rnk[t];
     };
     // 8 channels {32s + kperm(gq, e)} of one row: two 8-byte k reads, two
-    // 16-byte G reads (vector LDS accesses instead of per-element ones).
+    // 16-byte G reads.
     auto load_k8 = [&](int row, int s, float x[8]) {
         const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.r1.K[row][32 * s + 4 * gq]);
         const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.r1.K[row][32 * s + 16 + 4 * gq]);
@@ -419,32 +447,45 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         x[7] = g1.w;
     };
 
-    // ---- S3: Akk (-> L^T in LDS), Aqk and q e^G (-> fragments) --------------
+    // ---- S3: Akk (-> L^T), Aqk (-> LT's lower triangle), q e^G fragments ----
+    // Half sh = 1 stores its partial products into LT; after a barrier half
+    // sh = 0 adds its own (held in registers) and applies beta. Every LT
+    // element is written: block (J, I), J < I, holds Akk^T; block (I, J),
+    // J < I, holds Aqk; a diagonal block holds Akk^T above and Aqk on and
+    // below its diagonal.
+    f32x4 pk[2][4], pq[2][4];  // sh = 0 partials of pair (I, J): Akk, Aqk
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
-        if (ii >= nI) {
-            break;
-        }
-        const int I = I0 + ii;
+        const int I = ii == 0 ? IA : 3 - IA;
         const int ri = 16 * I + r;
-        // q row: widen, norm over all 128 channels (4 lane groups), scale
-        float qv[4][8];
+        // q row: widen this half's channels, norm over all 128 (4 lane groups
+        // x 4 slices), scale
+        float qv[2][8];
         float qss = 0.f;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const uint2 q0 = qraw[ii][s][0];
-            const uint2 q1 = qraw[ii][s][1];
-            qv[s][0] = __uint_as_float(q0.x << 16);
-            qv[s][1] = __uint_as_float(q0.x & 0xffff0000u);
-            qv[s][2] = __uint_as_float(q0.y << 16);
-            qv[s][3] = __uint_as_float(q0.y & 0xffff0000u);
-            qv[s][4] = __uint_as_float(q1.x << 16);
-            qv[s][5] = __uint_as_float(q1.x & 0xffff0000u);
-            qv[s][6] = __uint_as_float(q1.y << 16);
-            qv[s][7] = __uint_as_float(q1.y & 0xffff0000u);
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const uint2 q0 = qraw[ii][q4][0];
+            const uint2 q1 = qraw[ii][q4][1];
+            float x[8];
+            x[0] = __uint_as_float(q0.x << 16);
+            x[1] = __uint_as_float(q0.x & 0xffff0000u);
+            x[2] = __uint_as_float(q0.y << 16);
+            x[3] = __uint_as_float(q0.y & 0xffff0000u);
+            x[4] = __uint_as_float(q1.x << 16);
+            x[5] = __uint_as_float(q1.x & 0xffff0000u);
+            x[6] = __uint_as_float(q1.y << 16);
+            x[7] = __uint_as_float(q1.y & 0xffff0000u);
+            if (q4 < 2) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                qss += qv[s][e] * qv[s][e];
+                for (int e = 0; e < 8; ++e) {
+                    qv[q4][e] = x[e];
+                }
+            }
+            if (norm) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    qss += x[e] * x[e];
+                }
             }
         }
         float qscale = a.scale;
@@ -453,113 +494,114 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             qss += __shfl_xor(qss, 32);
             qscale = a.scale / sqrtf(qss + 1e-6f);
         }
-        // the block's anchor row G[16I][.], kept for every column block
-        float anc[4][8];
+        // the block's anchor row G[16I][.]
+        float anc[2][8];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            load_g8(16 * I, s, anc[s]);
+        for (int sl = 0; sl < 2; ++sl) {
+            load_g8(16 * I, 2 * sh + sl, anc[sl]);
         }
         const float rki = sm.rnk[ri];
-        bf16x8 Rh[4], Qh[4], Ql[4];
+        bf16x8 Rh[2], Qh[2], Ql[2];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int sl = 0; sl < 2; ++sl) {
+            const int s = 2 * sh + sl;
             float kk[8], gg[8], rv[8], qa[8], qg[8];
             load_k8(ri, s, kk);
             load_g8(ri, s, gg);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float ex = __expf(gg[e] - anc[s][e]);
-                const float qn = qv[s][e] * qscale;
+                const float ex = ex2(gg[e] - anc[sl][e]);
+                const float qn = qv[sl][e] * qscale;
                 rv[e] = kk[e] * rki * ex;
                 qa[e] = qn * ex;
-                qg[e] = qn * __expf(gg[e]);
+                qg[e] = qn * ex2(gg[e]);
             }
-            Rh[s] = to_bf16x8(rv);
-            split_bf16x8(qa, Qh[s], Ql[s]);
-            // q e^G fragment (mt = I, s); for I = 3 only wave 2 writes it
-            if (!(I == 3 && wave == 3)) {
-                bf16x8 fh, fl;
-                split_bf16x8(qg, fh, fl);
-                store_frag(rec, kOffQgH, I * 4 + s, lane, fh);
-                store_frag(rec, kOffQgL, I * 4 + s, lane, fl);
-            }
+            Rh[sl] = to_bf16x8(rv);
+            split_bf16x8(qa, Qh[sl], Ql[sl]);
+            bf16x8 fh, fl;
+            split_bf16x8(qg, fh, fl);
+            store_frag(rec, kOffQgH, I * 4 + s, lane, fh);
+            store_frag(rec, kOffQgL, I * 4 + s, lane, fl);
         }
-        // this wave's column blocks J of row block I
-        const int J0 = wave == 3 ? 2 : 0;
-        const int J1 = wave == 2 ? 1 : I;
-        float aq[4][4];
+        // pairs (I, J), J <= I, over this half's channels
 #pragma unroll
-        for (int J = 0; J < 4; ++J) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                aq[J][e] = 0.f;
-            }
-        }
-#pragma unroll
-        for (int J = 0; J < 4; ++J) {
-            if (J < J0 || J > J1) {
-                continue;
+        for (int J = 0; J < (ii == 0 ? 4 : 2); ++J) {
+            if (J > I) {
+                break;  // uniform per wave
             }
             const int rj = 16 * J + r;
             const float rkj = sm.rnk[rj];
-            const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-            f32x4 akk2[2] = {z4, z4};
-            f32x4 aq3[3] = {z4, z4, z4};
+            f32x4 akk = {0.f, 0.f, 0.f, 0.f};
+            f32x4 aqt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int sl = 0; sl < 2; ++sl) {
+                const int s = 2 * sh + sl;
                 float kk[8], gg[8], cv[8];
                 load_k8(rj, s, kk);
                 load_g8(rj, s, gg);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    cv[e] = kk[e] * rkj * __expf(anc[s][e] - gg[e]);
+                    cv[e] = kk[e] * rkj * ex2(anc[sl][e] - gg[e]);
                 }
                 bf16x8 Ch, Cl;
                 split_bf16x8(cv, Ch, Cl);
-                akk2[s & 1] = mfma(Rh[s], Ch, akk2[s & 1]);  // Akk[i][j], rows i of block I
-                aq3[0] = mfma(Ch, Qh[s], aq3[0]);            // Aqk^T[j][i]
-                aq3[1] = mfma(Ch, Ql[s], aq3[1]);
-                aq3[2] = mfma(Cl, Qh[s], aq3[2]);
+                akk = mfma(Rh[sl], Ch, akk);  // Akk[16I + 4gq + e][16J + r]
+                aqt = mfma(Ch, Qh[sl], aqt);  // Aqk[16I + r][16J + 4gq + e]
+                aqt = mfma(Ch, Ql[sl], aqt);
+                aqt = mfma(Cl, Qh[sl], aqt);
             }
-            f32x4 akk, aqt;
+            if (sh == 0) {
+                pk[ii][J] = akk;
+                pq[ii][J] = aqt;
+            } else if (J < I) {
+                // lane (r, gq) holds Akk[16I + 4gq + e][16J + r] and Aqk[16I + r][16J + 4gq + e]
+                *reinterpret_cast<f32x4 *>(&sm.LT[16 * J + r][16 * I + 4 * gq]) = akk;
+                *reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * J + 4 * gq]) = aqt;
+            } else {
+                f32x4 m;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                akk[e] = akk2[0][e] + akk2[1][e];
-                aqt[e] = (aq3[0][e] + aq3[1][e]) + aq3[2][e];
+                for (int e = 0; e < 4; ++e) {
+                    m[e] = r < 4 * gq + e ? akk[e] : aqt[e];
+                }
+                *reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * I + 4 * gq]) = m;
             }
-            float4 lt;
-            float *ltp = &lt.x;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = 16 * I + 4 * gq + e;
-                const int j = 16 * J + r;
-                ltp[e] = j < i ? akk[e] * sm.beta[i] : 0.f;
-                // aqt holds Aqk[16I + r][16J + 4gq + e]
-                aq[J][e] = (16 * J + 4 * gq + e) <= ri ? aqt[e] : 0.f;
-            }
-            *reinterpret_cast<float4 *>(&sm.LT[16 * J + r][16 * I + 4 * gq]) = lt;
         }
-        // Aqk fragments (mt = I, s): s covers column blocks 2s and 2s+1
+    }
+    lds_barrier();
+    if (sh == 0) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const bool mine = (2 * s >= J0 && 2 * s <= (J1 | 1)) || (I < 3 && s * 2 > I);
-            if (!mine) {
-                continue;
-            }
-            float x[8];
+        for (int ii = 0; ii < 2; ++ii) {
+            const int I = ii == 0 ? IA : 3 - IA;
+            const float4 b4 = *reinterpret_cast<const float4 *>(&sm.beta[16 * I + 4 * gq]);
+            const f32x4 bv = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[e] = aq[2 * s][e];
-                x[4 + e] = aq[2 * s + 1][e];
+            for (int J = 0; J < (ii == 0 ? 4 : 2); ++J) {
+                if (J > I) {
+                    break;
+                }
+                if (J < I) {
+                    f32x4 *pa = reinterpret_cast<f32x4 *>(&sm.LT[16 * J + r][16 * I + 4 * gq]);
+                    f32x4 *pb = reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * J + 4 * gq]);
+                    const f32x4 xa = *pa;
+                    const f32x4 xb = *pb;
+                    *pa = (xa + pk[ii][J]) * bv;
+                    *pb = xb + pq[ii][J];
+                } else {
+                    f32x4 *pd = reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * I + 4 * gq]);
+                    const f32x4 xd = *pd;
+                    f32x4 m;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        m[e] = r < 4 * gq + e ? (xd[e] + pk[ii][J][e]) * bv[e] : xd[e] + pq[ii][J][e];
+                    }
+                    *pd = m;
+                }
             }
-            bf16x8 fh, fl;
-            split_bf16x8(x, fh, fl);
-            store_frag(rec, kOffAqH, I * 2 + s, lane, fh);
-            store_frag(rec, kOffAqL, I * 2 + s, lane, fl);
         }
     }
 
-    // ---- S4: kd^T fragments, e^(G_last), tracking operands, (e^G k)^T -------
+
+    // ---- S4: kd^T fragments, e^(G_last), tracking operands, e^G k ----------
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         const int mk = 2 * wave + tt;
@@ -571,7 +613,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int t = 32 * s + kperm(gq, e);
-                x[e] = kval(t, k) * __expf(gl - sm.r0.G[t][k]);
+                x[e] = kval(t, k) * ex2(gl - sm.r0.G[t][k]);
             }
             bf16x8 fh, fl;
             split_bf16x8(x, fh, fl);
@@ -580,7 +622,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
     }
     if (tid < DK) {
-        reinterpret_cast<float *>(rec + kOffGl)[tid] = __expf(sm.r0.G[BT - 1][tid]);
+        reinterpret_cast<float *>(rec + kOffGl)[tid] = ex2(sm.r0.G[BT - 1][tid]);
     }
     // The tracked prefix inside this chunk (0 < rr < len): its state is
     // e^(G_{rr-1}) S + (e^(G_{rr-1} - G_t) k_t)_{t<rr}^T vnew.
@@ -601,7 +643,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int t = 32 * s + kperm(gq, e);
-                        x[e] = t < rr ? kval(t, k) * __expf(gr - sm.r0.G[t][k]) : 0.f;
+                        x[e] = t < rr ? kval(t, k) * ex2(gr - sm.r0.G[t][k]) : 0.f;
                     }
                     bf16x8 fh, fl;
                     split_bf16x8(x, fh, fl);
@@ -610,45 +652,30 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 }
             }
             if (tid < DK) {
-                reinterpret_cast<float *>(tr + kTrOffGl)[tid] = __expf(sm.r0.G[rr - 1][tid]);
+                reinterpret_cast<float *>(tr + kTrOffGl)[tid] = ex2(sm.r0.G[rr - 1][tid]);
             }
         }
     }
-    uint32_t kep[16];
-    {
-        const int k = tid & 127;
-        const int half = tid >> 7;
+    // e^G k rows rg + 8i, columns 4kc..4kc+3, as bf16 (written after the barrier)
+    uint2 kep[8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int t = half * 32 + 2 * i;
-            const uint16_t e0 = f32_to_bf16(kval(t, k) * __expf(sm.r0.G[t][k]));
-            const uint16_t e1 = f32_to_bf16(kval(t + 1, k) * __expf(sm.r0.G[t + 1][k]));
-            kep[i] = pack2(e0, e1);
-        }
+    for (int i = 0; i < 8; ++i) {
+        const int t = rg + 8 * i;
+        const uint2 k2 = *reinterpret_cast<const uint2 *>(&sm.r1.K[t][4 * kc]);
+        const float4 g4 = *reinterpret_cast<const float4 *>(&sm.r0.G[t][4 * kc]);
+        const float rn = sm.rnk[t];
+        kep[i].x = pack_bf16x2(__uint_as_float(k2.x << 16) * rn * ex2(g4.x),
+                               __uint_as_float(k2.x & 0xffff0000u) * rn * ex2(g4.y));
+        kep[i].y = pack_bf16x2(__uint_as_float(k2.y << 16) * rn * ex2(g4.z),
+                               __uint_as_float(k2.y & 0xffff0000u) * rn * ex2(g4.w));
     }
     lds_barrier();  // G and K are dead from here on
     {
-        const int k = tid & 127;
-        const int half = tid >> 7;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            *reinterpret_cast<uint32_t *>(&sm.r1.KE[swz(k, half * 32 + 2 * i)]) = kep[i];
-        }
-        // v^T (bf16, swizzled), rows zero-padded
-        const int kc = tid & 31;
-        const int rg = tid >> 5;
-        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int t = rg + 8 * i;
-            uint2 vr = make_uint2(0u, 0u);
-            if (t < len) {
-                vr = *reinterpret_cast<const uint2 *>(vp + (static_cast<int64_t>(t0 + t) * H + h) * DK + 4 * kc);
-            }
-            sm.r0.late.Vt[swz(4 * kc + 0, t)] = static_cast<uint16_t>(vr.x & 0xffffu);
-            sm.r0.late.Vt[swz(4 * kc + 1, t)] = static_cast<uint16_t>(vr.x >> 16);
-            sm.r0.late.Vt[swz(4 * kc + 2, t)] = static_cast<uint16_t>(vr.y & 0xffffu);
-            sm.r0.late.Vt[swz(4 * kc + 3, t)] = static_cast<uint16_t>(vr.y >> 16);
+            *reinterpret_cast<uint2 *>(&sm.r1.KE[t][4 * kc]) = kep[i];
+            *reinterpret_cast<uint2 *>(&sm.r0.late.V[t][4 * kc]) = vraw[i];
         }
         // X: upper blocks zero
         for (int idx = tid; idx < BT * BT; idx += kThreads) {
@@ -657,6 +684,23 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             if ((j >> 4) > (i >> 4)) {
                 sm.r0.late.X[i][j] = 0.f;
             }
+        }
+        // Aqk fragments (mt = wave, s): rows 16 wave + r, zero above the diagonal
+        const int row = 16 * wave + r;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.LT[row][32 * s + 4 * gq]);
+            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.LT[row][32 * s + 16 + 4 * gq]);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x[e] = 32 * s + kperm(gq, e) <= row ? xv[e] : 0.f;
+            }
+            bf16x8 fh, fl;
+            split_bf16x8(x, fh, fl);
+            store_frag(rec, kOffAqH, wave * 2 + s, lane, fh);
+            store_frag(rec, kOffAqL, wave * 2 + s, lane, fl);
         }
     }
 
@@ -699,43 +743,44 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
     }
     lds_barrier();
-    // Off-diagonal blocks by level d = I - J:
-    //   M_IJ = sum_{K=J}^{I-1} L_IK X_KJ,  X_IJ = -X_II M_IJ;
-    // M_IJ is parked (transposed) in the still-zero upper block (J, I).
+    // Off-diagonal blocks by level d = I - J, one (I, J) per wave (wave J),
+    // on the fp32 MFMA (v_mfma_f32_16x16x4_f32: lane (r, g) supplies A[r][g]
+    // and B[g][r] of each 4-wide K step; C as for the bf16 tiles):
+    //   M_IJ = sum_{K=J}^{I-1} L_IK X_KJ,   X_IJ = -X_II M_IJ.
+    // M_IJ passes through the wave's still-zero upper block (J, I) of X, which
+    // is cleared again before the level's barrier.
     for (int d = 1; d < 4; ++d) {
-        const int nb = 4 - d;
-        for (int idx = tid; idx < nb * 256; idx += kThreads) {
-            const int J = idx >> 8;
-            const int I = J + d;
-            const int i = (idx >> 4) & 15;
-            const int jj = idx & 15;
-            float acc = 0.f;
-#pragma unroll 16
-            for (int kk = 16 * J; kk < 16 * I; ++kk) {
-                acc += sm.LT[kk][16 * I + i] * sm.r0.late.X[kk][16 * J + jj];
-            }
-            sm.r0.late.X[16 * J + jj][16 * I + i] = acc;
-        }
-        lds_barrier();
-        for (int idx = tid; idx < nb * 256; idx += kThreads) {
-            const int J = idx >> 8;
-            const int I = J + d;
-            const int i = (idx >> 4) & 15;
-            const int jj = idx & 15;
-            float acc = 0.f;
+        const int J = wave;
+        const int I = J + d;
+        if (I < 4) {
+            f32x4 m = {0.f, 0.f, 0.f, 0.f};
+            for (int K = J; K < I; ++K) {
 #pragma unroll
-            for (int kk = 0; kk < 16; ++kk) {
-                acc += sm.r0.late.X[16 * I + i][16 * I + kk] * sm.r0.late.X[16 * J + jj][16 * I + kk];
+                for (int k4 = 0; k4 < 4; ++k4) {
+                    const int kk = 16 * K + 4 * k4 + gq;
+                    m = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.LT[kk][16 * I + r],
+                                                            sm.r0.late.X[kk][16 * J + r], m, 0, 0, 0);
+                }
             }
-            sm.r0.late.X[16 * I + i][16 * J + jj] = -acc;
-        }
-        lds_barrier();
-        for (int idx = tid; idx < nb * 256; idx += kThreads) {
-            const int J = idx >> 8;
-            const int I = J + d;
-            const int i = (idx >> 4) & 15;
-            const int jj = idx & 15;
-            sm.r0.late.X[16 * J + jj][16 * I + i] = 0.f;
+            // lane (r, gq) holds M[4gq + i][r]; park it row-major in block (J, I)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sm.r0.late.X[16 * J + 4 * gq + i][16 * I + r] = m[i];
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k4 = 0; k4 < 4; ++k4) {
+                x = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.r0.late.X[16 * I + r][16 * I + 4 * k4 + gq],
+                                                        sm.r0.late.X[16 * J + 4 * k4 + gq][16 * I + r], x,
+                                                        0, 0, 0);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sm.r0.late.X[16 * I + 4 * gq + i][16 * J + r] = -x[i];
+                sm.r0.late.X[16 * J + 4 * gq + i][16 * I + r] = 0.f;
+            }
         }
         lds_barrier();
     }
@@ -758,31 +803,23 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             split_bf16x8(x, Th[s], Tl[s]);
         }
-        // u tiles (mt = wave, vt): A = T rows, B = v (K = j)
+        // u tiles (mt = wave, vt): A = T rows, B = v (K = token)
 #pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
-            const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-            f32x4 acc[2] = {z4, z4};
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 if (s >= nS) {
                     break;  // uniform per wave; keeps s (and Th[s]) static
                 }
-                const int row = 16 * vt + r;
-                const uint2 v0 = *reinterpret_cast<const uint2 *>(&sm.r0.late.Vt[swz(row, 32 * s + 4 * gq)]);
-                const uint2 v1 = *reinterpret_cast<const uint2 *>(&sm.r0.late.Vt[swz(row, 32 * s + 16 + 4 * gq)]);
-                const bf16x8 vb = as_bf16x8(u32x4{v0.x, v0.y, v1.x, v1.y});
-                acc[0] = mfma(Th[s], vb, acc[0]);
-                acc[1] = mfma(Tl[s], vb, acc[1]);
+                const bf16x8 vb = lds_tr_frag(&sm.r0.late.V[0][0], 32 * s, 16 * vt, lane);
+                acc = mfma(Th[s], vb, acc);
+                acc = mfma(Tl[s], vb, acc);
             }
-            f32x4 uo;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uo[i] = acc[0][i] + acc[1][i];
-            }
-            reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = uo;
+            reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = acc;
         }
-        // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k, B = T^T (K = j)
+        // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k (K = token), B = T^T
+#pragma unroll
         for (int sp = 0; sp < 4; ++sp) {
             float x[8];
 #pragma unroll
@@ -794,10 +831,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                     if (s >= nS) {
                         break;
                     }
-                    const int row = 16 * mk + r;
-                    const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.r1.KE[swz(row, 32 * s + 4 * gq)]);
-                    const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.r1.KE[swz(row, 32 * s + 16 + 4 * gq)]);
-                    const bf16x8 kb = as_bf16x8(u32x4{k0.x, k0.y, k1.x, k1.y});
+                    const bf16x8 kb = lds_tr_frag(&sm.r1.KE[0][0], 32 * s, 16 * mk, lane);
                     acc = mfma(kb, Th[s], acc);
                 }
                 // acc[i] = w[16*wave + r][16*mk + 4gq + i]
@@ -813,12 +847,27 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 
 // ---------------------------------------------------------------------------
 // K2: the serial chunk scan per (sequence, head, 16 value columns).
+//
+// Eight waves in two roles, so every SIMD holds two independent instruction
+// streams:
+//   chain waves 0-3  own S rows [32c, 32c+32) (fp32, registers) and run the
+//                    recurrence: publish S_j, vnew_j = u - w S_j, publish
+//                    vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j;
+//   output waves 4-7 own token rows [16o, 16o+16) and compute
+//                    o_j = (q e^G) S_j + Aqk vnew_j one phase behind the chain.
+// Per chunk j there are two workgroup barriers: B1(j) after S_j is published,
+// B2(j) after vnew_j is published. S_j and vnew_j live in LDS buffers indexed
+// by j's parity. Output waves compute (q e^G) S_j between B2(j) and B1(j+1)
+// (while the chain runs its state update) and add Aqk vnew_j between B1(j+1)
+// and B2(j+1); buffer j&1 is rewritten only at chunk j+2, after both.
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws) {
-    __shared__ u32x4 sfrag[4][2][64];     // S as B fragments, slice s = k rows [32s, 32s+32)
-    __shared__ uint32_t vfrag[2][2][64][4];  // vnew as B fragments, slice s = tokens [32s, 32s+32)
-    __shared__ uint32_t otile[4][16][8];     // per wave: its 16 output rows x 16 bf16 columns
+constexpr int kScanThreads = 512;
+
+__global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws) {
+    __shared__ u32x4 sbuf[2][4][2][64];         // S_j as B fragments: [parity][slice][hi, lo][lane]
+    __shared__ uint32_t vbuf[2][2][2][64][4];   // vnew_j as B fragments: [parity][slice][hi, lo]
+    __shared__ uint32_t otile[4][16][8];        // per output wave: 16 rows x 16 bf16 columns
 
     const int H = a.num_heads;
     const int N = a.num_seqs;
@@ -844,257 +893,307 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    // wave index as a scalar: the role branch below must be wave-uniform, since
+    // both roles meet at the same workgroup barriers
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = w & 3;
     const int r = lane & 15;
     const int gq = lane >> 4;
     const int vcol = 16 * vt + r;
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    uint16_t *out = static_cast<uint16_t *>(a.out);
+    auto rec_of = [&](int j) {
+        return ws + LY.recs + (static_cast<size_t>(c0 + j) * H + h) * kRecBytes;
+    };
 
-    int slot = a.state_indices[n];
-    if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
-        slot = 0;
-    }
-    int track_slot = 0;
-    int track_len = -1;
-    if (a.track_indices != nullptr) {
-        track_slot = a.track_indices[n];
-        if (track_slot <= 0 || static_cast<int64_t>(track_slot) >= a.num_slots) {
-            track_slot = 0;
-        } else {
-            track_len = a.track_lens[n];
+    if (w < 4) {
+        // ------------------------------- chain waves -------------------------------
+        int slot = a.state_indices[n];
+        if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
+            slot = 0;
         }
-    }
-    const int64_t head_off = static_cast<int64_t>(h) * a.state_stride_head;
+        int track_slot = 0;
+        int track_len = -1;
+        if (a.track_indices != nullptr) {
+            track_slot = a.track_indices[n];
+            if (track_slot <= 0 || static_cast<int64_t>(track_slot) >= a.num_slots) {
+                track_slot = 0;
+            } else {
+                track_len = a.track_lens[n];
+            }
+        }
+        const int64_t head_off = static_cast<int64_t>(h) * a.state_stride_head;
 
-    // S rows k in [32w, 32w+32): tiles kt = 2w + tt, lane holds S[16kt + 4gq + i][vcol].
-    f32x4 S[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        if (slot > 0) {
-            const float *src = a.state + slot * a.state_stride_slot + head_off +
-                               static_cast<int64_t>(vcol) * DK + 16 * (2 * w + tt) + 4 * gq;
-            const float4 s4 = load4(src);
-            S[tt] = f32x4{s4.x, s4.y, s4.z, s4.w};
-        } else {
-            S[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    auto store_S = [&](int dst_slot, const f32x4 *val) {
+        // S rows [32wr, 32wr+32): tiles kt = 2wr + tt, lane holds S[16kt + 4gq + i][vcol].
+        f32x4 S[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            float *dst = a.state + dst_slot * a.state_stride_slot + head_off +
-                         static_cast<int64_t>(vcol) * DK + 16 * (2 * w + tt) + 4 * gq;
-            *reinterpret_cast<float4 *>(dst) = make_float4(val[tt][0], val[tt][1], val[tt][2], val[tt][3]);
+            if (slot > 0) {
+                const float *src = a.state + slot * a.state_stride_slot + head_off +
+                                   static_cast<int64_t>(vcol) * DK + 16 * (2 * wr + tt) + 4 * gq;
+                const float4 s4 = load4(src);
+                S[tt] = f32x4{s4.x, s4.y, s4.z, s4.w};
+            } else {
+                S[tt] = z4;
+            }
         }
-    };
-    if (track_slot > 0 && track_len == 0) {
-        store_S(track_slot, S);
-    }
-
-    uint16_t *out = static_cast<uint16_t *>(a.out);
-    const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
-
-    // One chunk's operands, held in registers. Two sets alternate so the
-    // next chunk's fragments are in flight while this chunk computes.
-    struct Ops {
-        bf16x8 Wf[4], Qh[4], Ql[4], Ah[2], Al[2], Kh[2][2], Kl[2][2];
-        f32x4 u, gl[2];
-    };
-    auto load_ops = [&](Ops &op, int j) {
-        const char *rec = ws + LY.recs + (static_cast<size_t>(c0 + j) * H + h) * kRecBytes;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            op.Wf[s] = load_frag(rec, kOffW, w * 4 + s, lane);
-            op.Qh[s] = load_frag(rec, kOffQgH, w * 4 + s, lane);
-            op.Ql[s] = load_frag(rec, kOffQgL, w * 4 + s, lane);
-        }
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            op.Ah[s] = load_frag(rec, kOffAqH, w * 2 + s, lane);
-            op.Al[s] = load_frag(rec, kOffAqL, w * 2 + s, lane);
+        auto store_S = [&](int dst_slot, const f32x4 *val) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                op.Kh[tt][s] = load_frag(rec, kOffKdH, (2 * w + tt) * 2 + s, lane);
-                op.Kl[tt][s] = load_frag(rec, kOffKdL, (2 * w + tt) * 2 + s, lane);
+                float *dst = a.state + dst_slot * a.state_stride_slot + head_off +
+                             static_cast<int64_t>(vcol) * DK + 16 * (2 * wr + tt) + 4 * gq;
+                *reinterpret_cast<float4 *>(dst) =
+                    make_float4(val[tt][0], val[tt][1], val[tt][2], val[tt][3]);
             }
+        };
+        if (track_slot > 0 && track_len == 0) {
+            store_S(track_slot, S);
         }
-        op.u = reinterpret_cast<const f32x4 *>(rec + kOffU)[(w * 8 + vt) * 64 + lane];
+        const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
+
+        // One chunk's chain operands; two sets alternate so the next chunk's
+        // fragments are in flight while this chunk computes.
+        struct Ops {
+            bf16x8 Wf[4], Kh[2][2], Kl[2][2];
+            f32x4 u, gl[2];
+        };
+        auto load_ops = [&](Ops &op, int j) {
+            const char *rec = rec_of(j);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            op.gl[tt] = *reinterpret_cast<const f32x4 *>(rec + kOffGl + 4 * (16 * (2 * w + tt) + 4 * gq));
+            for (int s = 0; s < 4; ++s) {
+                op.Wf[s] = load_frag(rec, kOffW, wr * 4 + s, lane);
+            }
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    op.Kh[tt][s] = load_frag(rec, kOffKdH, (2 * wr + tt) * 2 + s, lane);
+                    op.Kl[tt][s] = load_frag(rec, kOffKdL, (2 * wr + tt) * 2 + s, lane);
+                }
+            }
+            op.u = reinterpret_cast<const f32x4 *>(rec + kOffU)[(wr * 8 + vt) * 64 + lane];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                op.gl[tt] = *reinterpret_cast<const f32x4 *>(rec + kOffGl +
+                                                             4 * (16 * (2 * wr + tt) + 4 * gq));
+            }
+        };
+
+        auto step = [&](const Ops &op, int j) {
+            const int p = j & 1;
+            const int len = eos - (bos + BT * j) < BT ? eos - (bos + BT * j) : BT;
+            // A. publish S_j (slice wr) as hi/lo B fragments
+            {
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    x[i] = S[0][i];
+                    x[4 + i] = S[1][i];
+                }
+                bf16x8 hi, lo;
+                split_bf16x8(x, hi, lo);
+                sbuf[p][wr][0][lane] = as_u32x4(hi);
+                sbuf[p][wr][1][lane] = as_u32x4(lo);
+            }
+            lds_barrier();  // B1(j)
+            // B. vnew rows [16wr, 16wr+16) = u - w S_j (single pass), published hi/lo
+            {
+                f32x4 acc = z4;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    acc = mfma(op.Wf[s], as_bf16x8(sbuf[p][s][0][lane]), acc);
+                }
+                uint32_t hp[2], lp[2];
+#pragma unroll
+                for (int q2 = 0; q2 < 2; ++q2) {
+                    const float v0 = op.u[2 * q2] - acc[2 * q2];
+                    const float v1 = op.u[2 * q2 + 1] - acc[2 * q2 + 1];
+                    hp[q2] = pack_bf16x2(v0, v1);
+                    lp[q2] = pack_bf16x2(v0 - __uint_as_float(hp[q2] << 16),
+                                         v1 - __uint_as_float(hp[q2] & 0xffff0000u));
+                }
+                // tile mt = wr is half wr%2 of slice wr/2
+                const int sl = wr >> 1;
+                const int hf = (wr & 1) * 2;
+                vbuf[p][sl][0][lane][hf] = hp[0];
+                vbuf[p][sl][0][lane][hf + 1] = hp[1];
+                vbuf[p][sl][1][lane][hf] = lp[0];
+                vbuf[p][sl][1][lane][hf + 1] = lp[1];
+            }
+            lds_barrier();  // B2(j)
+            // C. S_{j+1} = e^(G_last) S_j + kd^T vnew_j (3-pass)
+            bf16x8 vh[2], vl[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                vh[s] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][lane][0]));
+                vl[s] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][lane][0]));
+            }
+            // tracked prefix strictly inside this chunk
+            const int rr = track_len - BT * j;
+            if (track_slot > 0 && rr > 0 && rr < len) {
+                f32x4 St[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const f32x4 g2 = *reinterpret_cast<const f32x4 *>(
+                        tr + kTrOffGl + 4 * (16 * (2 * wr + tt) + 4 * gq));
+                    f32x4 tu = z4;
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        const bf16x8 th = load_frag(tr, kTrOffKdH, (2 * wr + tt) * 2 + s, lane);
+                        const bf16x8 tl = load_frag(tr, kTrOffKdL, (2 * wr + tt) * 2 + s, lane);
+                        tu = mfma(th, vh[s], tu);
+                        tu = mfma(th, vl[s], tu);
+                        tu = mfma(tl, vh[s], tu);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        St[tt][i] = S[tt][i] * g2[i] + tu[i];
+                    }
+                }
+                store_S(track_slot, St);
+            }
+            f32x4 su[2] = {z4, z4};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    su[tt] = mfma(op.Kh[tt][s], vh[s], su[tt]);
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    su[tt] = mfma(op.Kh[tt][s], vl[s], su[tt]);
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    su[tt] = mfma(op.Kl[tt][s], vh[s], su[tt]);
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    S[tt][i] = S[tt][i] * op.gl[tt][i] + su[tt][i];
+                }
+            }
+            if (track_slot > 0 && rr == len) {
+                store_S(track_slot, S);
+            }
+        };
+
+        // The prefetches are unconditional (clamped to the last chunk) so the
+        // compiler's wait counts stay exact on every path through the loop.
+        Ops opA, opB;
+        if (nch > 0) {
+            load_ops(opA, 0);
         }
-    };
-
-    auto step = [&](const Ops &op, int j) {
-        const int t0 = bos + BT * j;
-        const int len = eos - t0 < BT ? eos - t0 : BT;
-
-        // 1. publish S (slice s = w) as hi/lo B fragments
-        {
-            float x[8];
+        for (int j = 0; j < nch; j += 2) {
+            load_ops(opB, j + 1 < nch ? j + 1 : nch - 1);
+            step(opA, j);
+            if (j + 1 >= nch) {
+                break;
+            }
+            load_ops(opA, j + 2 < nch ? j + 2 : nch - 1);
+            step(opB, j + 1);
+        }
+        if (slot > 0) {
+            store_S(slot, S);
+        }
+    } else {
+        // ------------------------------- output waves ------------------------------
+        struct OpsO {
+            bf16x8 Qh[4], Ql[4], Ah[2], Al[2];
+        };
+        auto load_out = [&](OpsO &op, int j) {
+            const char *rec = rec_of(j);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                op.Qh[s] = load_frag(rec, kOffQgH, wr * 4 + s, lane);
+                op.Ql[s] = load_frag(rec, kOffQgL, wr * 4 + s, lane);
+            }
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                op.Ah[s] = load_frag(rec, kOffAqH, wr * 2 + s, lane);
+                op.Al[s] = load_frag(rec, kOffAqL, wr * 2 + s, lane);
+            }
+        };
+        f32x4 P = z4;  // (q e^G) S of the chunk whose output is pending
+        // o_j = P + Aqk vnew_j (3-pass); rows t < len of chunk j are stored,
+        // transposed through this wave's LDS tile so each lane writes 4
+        // consecutive columns of one row (one 8-byte nontemporal store).
+        auto finish = [&](const OpsO &op, int j) {
+            const int p = j & 1;
+            f32x4 acc = P;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][lane][0]));
+                const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][lane][0]));
+                acc = mfma(op.Ah[s], vh, acc);
+                acc = mfma(op.Ah[s], vl, acc);
+                acc = mfma(op.Al[s], vh, acc);
+            }
+            const int t0 = bos + BT * j;
+            const int len = eos - t0 < BT ? eos - t0 : BT;
+            uint16_t *ot = reinterpret_cast<uint16_t *>(&otile[wr][0][0]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                x[i] = S[0][i];
-                x[4 + i] = S[1][i];
-            }
-            bf16x8 hi, lo;
-            split_bf16x8(x, hi, lo);
-            sfrag[w][0][lane] = as_u32x4(hi);
-            sfrag[w][1][lane] = as_u32x4(lo);
-        }
-        lds_barrier();
-
-        // 2. vnew rows [16w, 16w+16) = u - w S ; 3. o = (q e^G) S (3-pass).
-        // Independent accumulators (per pass, per slice parity) keep several
-        // MFMA chains in flight: with one wave per SIMD a single dependent
-        // chain would pay the full MFMA latency on every link.
-        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-        f32x4 wsa[2] = {z4, z4};
-        f32x4 oq[3] = {z4, z4, z4};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const bf16x8 sh = as_bf16x8(sfrag[s][0][lane]);
-            const bf16x8 sl = as_bf16x8(sfrag[s][1][lane]);
-            wsa[s & 1] = mfma(op.Wf[s], sh, wsa[s & 1]);
-            oq[0] = mfma(op.Qh[s], sh, oq[0]);
-            oq[1] = mfma(op.Qh[s], sl, oq[1]);
-            oq[2] = mfma(op.Ql[s], sh, oq[2]);
-        }
-        f32x4 vn;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            vn[i] = op.u[i] - (wsa[0][i] + wsa[1][i]);
-        }
-        // 4. publish vnew (tile mt = w is half w%2 of slice w/2)
-        {
-            uint32_t hp[2], lp[2];
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                hp[p] = pack_bf16x2(vn[2 * p], vn[2 * p + 1]);
-                lp[p] = pack_bf16x2(vn[2 * p] - __uint_as_float(hp[p] << 16),
-                                    vn[2 * p + 1] - __uint_as_float(hp[p] & 0xffff0000u));
-            }
-            const int sl = w >> 1;
-            const int hf = (w & 1) * 2;
-            vfrag[sl][0][lane][hf] = hp[0];
-            vfrag[sl][0][lane][hf + 1] = hp[1];
-            vfrag[sl][1][lane][hf] = lp[0];
-            vfrag[sl][1][lane][hf + 1] = lp[1];
-        }
-        lds_barrier();
-
-        bf16x8 vh[2], vl[2];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            vh[s] = as_bf16x8(u32x4{vfrag[s][0][lane][0], vfrag[s][0][lane][1], vfrag[s][0][lane][2],
-                                    vfrag[s][0][lane][3]});
-            vl[s] = as_bf16x8(u32x4{vfrag[s][1][lane][0], vfrag[s][1][lane][1], vfrag[s][1][lane][2],
-                                    vfrag[s][1][lane][3]});
-        }
-        // 5. o += Aqk vnew (3-pass) and store rows t < len
-        f32x4 oa[3] = {z4, z4, z4};
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            oa[0] = mfma(op.Ah[s], vh[s], oa[0]);
-            oa[1] = mfma(op.Ah[s], vl[s], oa[1]);
-            oa[2] = mfma(op.Al[s], vh[s], oa[2]);
-        }
-        f32x4 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o[i] = ((oq[0][i] + oq[1][i]) + oq[2][i]) + ((oa[0][i] + oa[1][i]) + oa[2][i]);
-        }
-        // Output rows [16w, 16w+16) x 16 columns: transposed through this
-        // wave's own LDS tile so each lane stores 4 consecutive columns of one
-        // row (one 8-byte nontemporal store per lane instead of four 2-byte
-        // stores; no workgroup barrier -- the tile is private to the wave).
-        {
-            uint16_t *ot = reinterpret_cast<uint16_t *>(&otile[w][0][0]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ot[(4 * gq + i) * 16 + r] = f32_to_bf16(o[i]);
+                ot[(4 * gq + i) * 16 + r] = f32_to_bf16(acc[i]);
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             const int row = lane >> 2;
             const int cq = lane & 3;
             typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-            const u32x2 val = *reinterpret_cast<const u32x2 *>(&otile[w][row][2 * cq]);
-            const int t = 16 * w + row;
+            const u32x2 val = *reinterpret_cast<const u32x2 *>(&otile[wr][row][2 * cq]);
+            const int t = 16 * wr + row;
             if (t < len) {
                 __builtin_nontemporal_store(
                     val, reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(t0 + t) * H + h) * DK +
                                                    16 * vt + 4 * cq));
             }
-        }
-        // tracked prefix strictly inside this chunk
-        const int rr = track_len - BT * j;
-        if (track_slot > 0 && rr > 0 && rr < len) {
-            f32x4 St[2];
+        };
+        // P = (q e^G) S_j (3-pass), rows [16wr, 16wr+16)
+        auto start = [&](const OpsO &op, int j) {
+            const int p = j & 1;
+            f32x4 acc = z4;
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const f32x4 g2 = *reinterpret_cast<const f32x4 *>(tr + kTrOffGl +
-                                                                  4 * (16 * (2 * w + tt) + 4 * gq));
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    St[tt][i] = S[tt][i] * g2[i];
-                }
-                f32x4 tu[3] = {z4, z4, z4};
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const bf16x8 th = load_frag(tr, kTrOffKdH, (2 * w + tt) * 2 + s, lane);
-                    const bf16x8 tl = load_frag(tr, kTrOffKdL, (2 * w + tt) * 2 + s, lane);
-                    tu[0] = mfma(th, vh[s], tu[0]);
-                    tu[1] = mfma(th, vl[s], tu[1]);
-                    tu[2] = mfma(tl, vh[s], tu[2]);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    St[tt][i] += (tu[0][i] + tu[1][i]) + tu[2][i];
-                }
+            for (int s = 0; s < 4; ++s) {
+                const bf16x8 sh = as_bf16x8(sbuf[p][s][0][lane]);
+                const bf16x8 sl = as_bf16x8(sbuf[p][s][1][lane]);
+                acc = mfma(op.Qh[s], sh, acc);
+                acc = mfma(op.Qh[s], sl, acc);
+                acc = mfma(op.Ql[s], sh, acc);
             }
-            store_S(track_slot, St);
-        }
-        // 6. S <- e^(G_last) S + kd^T vnew (3-pass, independent chains)
-        f32x4 su[2][3] = {{z4, z4, z4}, {z4, z4, z4}};
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                su[tt][0] = mfma(op.Kh[tt][s], vh[s], su[tt][0]);
-                su[tt][1] = mfma(op.Kh[tt][s], vl[s], su[tt][1]);
-                su[tt][2] = mfma(op.Kl[tt][s], vh[s], su[tt][2]);
+            P = acc;
+        };
+        // Iteration j: [B1(j)] finish chunk j-1 (operands in `other`), load
+        // chunk j+1 into `other`, [B2(j)] start chunk j (operands in `cur`).
+        auto iter = [&](const OpsO &cur, OpsO &other, int j) {
+            lds_barrier();  // B1(j)
+            if (j > 0) {
+                finish(other, j - 1);
             }
-        }
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                S[tt][i] = S[tt][i] * op.gl[tt][i] + ((su[tt][0][i] + su[tt][1][i]) + su[tt][2][i]);
+            load_out(other, j + 1 < nch ? j + 1 : nch - 1);
+            lds_barrier();  // B2(j)
+            start(cur, j);
+            if (j == nch - 1) {
+                finish(cur, j);
             }
+        };
+        OpsO opA, opB;
+        if (nch > 0) {
+            load_out(opA, 0);
         }
-        if (track_slot > 0 && rr == len) {
-            store_S(track_slot, S);
+        for (int j = 0; j < nch; j += 2) {
+            iter(opA, opB, j);
+            if (j + 1 >= nch) {
+                break;
+            }
+            iter(opB, opA, j + 1);
         }
-    };
-
-    // The prefetches are unconditional (clamped to the last chunk) so the
-    // compiler's wait counts stay exact on every path through the loop.
-    Ops opA, opB;
-    if (nch > 0) {
-        load_ops(opA, 0);
-    }
-    for (int j = 0; j < nch; j += 2) {
-        load_ops(opB, j + 1 < nch ? j + 1 : nch - 1);
-        step(opA, j);
-        if (j + 1 >= nch) {
-            break;
-        }
-        load_ops(opA, j + 2 < nch ? j + 2 : nch - 1);
-        step(opB, j + 1);
     }
 
     // Tokens outside every sequence are written as zero.
     auto zero_rows = [&](int ta, int tb) {
-        for (int t = ta + tid / 16; t < tb; t += kThreads / 16) {
+        for (int t = ta + tid / 16; t < tb; t += kScanThreads / 16) {
             if ((tid & 15) == 0) {
                 // one thread per token row writes this tile's 16 columns
                 for (int cidx = 0; cidx < 16; ++cidx) {
@@ -1108,9 +1207,6 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const KdaChunkArgs
     }
     if (n == N - 1) {
         zero_rows(eos, a.num_tokens);
-    }
-    if (slot > 0) {
-        store_S(slot, S);
     }
 }
 
@@ -1199,7 +1295,7 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
         const char *cws = ws;
         void *params[] = {&kargs, &cws};
         if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_scan_kernel),
-                            dim3(static_cast<unsigned>(blocks)), dim3(kThreads), params, 0,
+                            dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads), params, 0,
                             st) != hipSuccess) {
             return KDA_ERR_LAUNCH;
         }
