@@ -221,6 +221,15 @@ constexpr int kPadX = 68;   // fp32 row stride of [64][64] tiles (16-B rows)
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// All-ones if `keep`, else zero, opaque to the optimizer: a value masked with
+// it is used unconditionally, so its load cannot be sunk into a branch (a
+// load under a per-lane branch is waited for before the next one issues).
+__device__ __forceinline__ uint32_t keep_mask(bool keep) {
+    uint32_t m = keep ? 0xffffffffu : 0u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -315,11 +324,24 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             const int s = q4 < 2 ? 2 * sh + q4 : 2 * (1 - sh) + (q4 - 2);
             qraw[ii][q4][0] = make_uint2(0u, 0u);
             qraw[ii][q4][1] = make_uint2(0u, 0u);
-            if (t < len && (q4 < 2 || norm)) {
-                const uint16_t *row = qp + (static_cast<int64_t>(t0 + t) * H + h) * DK + 32 * s;
+            if (q4 < 2 || norm) {  // uniform
+                const int tc = t < len ? t : len - 1;
+                const uint16_t *row = qp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + 32 * s;
                 qraw[ii][q4][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
                 qraw[ii][q4][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
             }
+        }
+    }
+    // padding rows of q are zeroed (loaded from a row clamped into the chunk)
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const uint32_t keep = keep_mask(16 * (ii == 0 ? IA : 3 - IA) + r < len);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            qraw[ii][q4][0].x &= keep;
+            qraw[ii][q4][0].y &= keep;
+            qraw[ii][q4][1].x &= keep;
+            qraw[ii][q4][1].y &= keep;
         }
     }
 
@@ -336,29 +358,50 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             expA = expf(a.A_log[h]);
             dtb = load4(a.dt_bias + static_cast<int64_t>(h) * DK + 4 * kc);
         }
+        // Loads are unconditional, from a row clamped into the chunk (a chunk
+        // holds at least one token); padding rows are zeroed afterwards.
+        // beta of row (tid & 63), used by the first wave
+        const int tb = (tid & 63) < len ? (tid & 63) : len - 1;
+        float braw;
+        if constexpr (GATE == KDA_GATE_RAW) {
+            braw = bf16_to_f32(static_cast<const uint16_t *>(a.beta)[static_cast<int64_t>(t0 + tb) * H + h]);
+        } else {
+            braw = static_cast<const float *>(a.beta)[static_cast<int64_t>(t0 + tb) * H + h];
+        }
         uint2 kraw[8];
         float4 g4[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int t = rg + 8 * i;
-            const int64_t base = (static_cast<int64_t>(t0 + t) * H + h) * DK + 4 * kc;
-            kraw[i] = make_uint2(0u, 0u);
-            vraw[i] = make_uint2(0u, 0u);
-            g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t < len) {
-                kraw[i] = *reinterpret_cast<const uint2 *>(kp + base);
-                vraw[i] = *reinterpret_cast<const uint2 *>(vp + base);
-                if constexpr (GATE == KDA_GATE_RAW) {
-                    const float4 av = load4(static_cast<const uint16_t *>(a.gate) + base);
-                    const float lb = a.lower_bound;
-                    g4[i].x = lb / (1.0f + __expf(-(expA * (av.x + dtb.x))));
-                    g4[i].y = lb / (1.0f + __expf(-(expA * (av.y + dtb.y))));
-                    g4[i].z = lb / (1.0f + __expf(-(expA * (av.z + dtb.z))));
-                    g4[i].w = lb / (1.0f + __expf(-(expA * (av.w + dtb.w))));
-                } else {
-                    g4[i] = load4(static_cast<const float *>(a.gate) + base);
-                }
+            const int tc = t < len ? t : len - 1;
+            const int64_t base = (static_cast<int64_t>(t0 + tc) * H + h) * DK + 4 * kc;
+            kraw[i] = *reinterpret_cast<const uint2 *>(kp + base);
+            vraw[i] = *reinterpret_cast<const uint2 *>(vp + base);
+            if constexpr (GATE == KDA_GATE_RAW) {
+                g4[i] = load4(static_cast<const uint16_t *>(a.gate) + base);
+            } else {
+                g4[i] = load4(static_cast<const float *>(a.gate) + base);
             }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t keep = keep_mask(rg + 8 * i < len);
+            kraw[i].x &= keep;
+            kraw[i].y &= keep;
+            vraw[i].x &= keep;
+            vraw[i].y &= keep;
+            if constexpr (GATE == KDA_GATE_RAW) {
+                const float4 av = g4[i];
+                const float lb = a.lower_bound;
+                g4[i].x = lb / (1.0f + __expf(-(expA * (av.x + dtb.x))));
+                g4[i].y = lb / (1.0f + __expf(-(expA * (av.y + dtb.y))));
+                g4[i].z = lb / (1.0f + __expf(-(expA * (av.z + dtb.z))));
+                g4[i].w = lb / (1.0f + __expf(-(expA * (av.w + dtb.w))));
+            }
+            g4[i].x = __uint_as_float(__float_as_uint(g4[i].x) & keep);
+            g4[i].y = __uint_as_float(__float_as_uint(g4[i].y) & keep);
+            g4[i].z = __uint_as_float(__float_as_uint(g4[i].z) & keep);
+            g4[i].w = __uint_as_float(__float_as_uint(g4[i].w) & keep);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -380,16 +423,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 make_float4(g4[i].x * kLog2e, g4[i].y * kLog2e, g4[i].z * kLog2e, g4[i].w * kLog2e);
         }
         if (tid < BT) {
-            float b = 0.f;
-            if (tid < len) {
-                const int64_t bi = static_cast<int64_t>(t0 + tid) * H + h;
-                if constexpr (GATE == KDA_GATE_RAW) {
-                    b = 1.0f / (1.0f + __expf(-bf16_to_f32(static_cast<const uint16_t *>(a.beta)[bi])));
-                } else {
-                    b = static_cast<const float *>(a.beta)[bi];
-                }
+            float b = braw;
+            if constexpr (GATE == KDA_GATE_RAW) {
+                b = 1.0f / (1.0f + __expf(-b));
             }
-            sm.beta[tid] = b;
+            sm.beta[tid] = tid < len ? b : 0.f;
         }
     }
     lds_barrier();
