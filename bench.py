@@ -53,10 +53,10 @@ DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
 # The kernel-trace/PMC summaries are kept under profiles/.
 FETCH_SCALE = 524288.0 / 262156.8
 WRITE_SCALE = 524288.0 / 524288.0
-DEC_FETCH_KIB, DEC_WRITE_KIB = 271558.7, 526401.0
+DEC_FETCH_KIB, DEC_WRITE_KIB = 267456.0, 526342.9
 DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
-PF_TRAFFIC = ((180848.0 + 264263.9) * FETCH_SCALE + (526336.0 + 108322.7) * WRITE_SCALE) * 1024
+PF_TRAFFIC = ((180759.8 + 276671.1) * FETCH_SCALE + (526336.1 + 79101.2) * WRITE_SCALE) * 1024
 
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
@@ -279,7 +279,7 @@ def main():
         roofline=dict(
             bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
             frac=achieved / HBM_PEAK_GBS, traffic=DEC_TRAFFIC,
-            kernel="recurrent_kernel<128,8,bf16,bf16,LOG>",
+            kernel="recurrent_kernel<128,4,bf16,bf16,LOG>",
             algorithmic_bytes_per_launch=DEC_BYTES, kernel_us=dec["kernel_us"],
         ),
         prefill=prefill,
