@@ -130,35 +130,67 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     const TV *vp = static_cast<const TV *>(a.v);
     TV *op = static_cast<TV *>(a.out);
 
-    for (int t = bos; t < eos; ++t) {
+    // One token's inputs, as loaded (gates are transformed at use). The next
+    // token's are loaded while the current one computes: a multi-token
+    // sequence (verify, prefill) would otherwise wait a full load latency per
+    // token. The branches on `more` are uniform across the workgroup.
+    struct TokenIn {
+        float4 q, k, g;
+        float v[NP];
+        float b;
+    };
+    auto fetch = [&](int t, TokenIn &in) {
         const int64_t base = (static_cast<int64_t>(t) * H + head) * D;
-        float4 qv = load4(qp + base + 4 * kc);
-        float4 kv = load4(kp + base + 4 * kc);
+        in.q = load4(qp + base + 4 * kc);
+        in.k = load4(kp + base + 4 * kc);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            in.v[p] = load1(vp + base + row0 + p * RPP);
+        }
+        const int64_t bi = static_cast<int64_t>(t) * H + head;
+        if constexpr (GATE == KDA_GATE_RAW) {
+            in.g = load4(static_cast<const uint16_t *>(a.gate) + base + 4 * kc);
+            in.b = bf16_to_f32(static_cast<const uint16_t *>(a.beta)[bi]);
+        } else {
+            in.g = load4(static_cast<const float *>(a.gate) + base + 4 * kc);
+            in.b = static_cast<const float *>(a.beta)[bi];
+        }
+    };
+    TokenIn cur, nxt;
+    if (bos < eos) {
+        fetch(bos, cur);
+    }
+    for (int t = bos; t < eos; ++t) {
+        const bool more = t + 1 < eos;
+        if (more) {
+            fetch(t + 1, nxt);
+        }
+        const int64_t base = (static_cast<int64_t>(t) * H + head) * D;
+        float4 qv = cur.q;
+        float4 kv = cur.k;
         float vr[NP];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            vr[p] = load1(vp + base + row0 + p * RPP);
+            vr[p] = cur.v[p];
         }
         float4 dec;
         float beta;
         if constexpr (GATE == KDA_GATE_RAW) {
-            const float4 av = load4(static_cast<const uint16_t *>(a.gate) + base + 4 * kc);
+            const float4 av = cur.g;
             const float lb = a.lower_bound;
             // g = lower_bound / (1 + exp(-(exp(A_log) * (a + dt_bias)))), decay = exp(g)
             dec.x = expf(lb / (1.0f + expf(-(expA * (av.x + dtb.x)))));
             dec.y = expf(lb / (1.0f + expf(-(expA * (av.y + dtb.y)))));
             dec.z = expf(lb / (1.0f + expf(-(expA * (av.z + dtb.z)))));
             dec.w = expf(lb / (1.0f + expf(-(expA * (av.w + dtb.w)))));
-            const float b =
-                bf16_to_f32(static_cast<const uint16_t *>(a.beta)[static_cast<int64_t>(t) * H + head]);
-            beta = 1.0f / (1.0f + expf(-b));
+            beta = 1.0f / (1.0f + expf(-cur.b));
         } else if constexpr (GATE == KDA_GATE_LOG) {
-            const float4 gv = load4(static_cast<const float *>(a.gate) + base + 4 * kc);
+            const float4 gv = cur.g;
             dec = make_float4(expf(gv.x), expf(gv.y), expf(gv.z), expf(gv.w));
-            beta = static_cast<const float *>(a.beta)[static_cast<int64_t>(t) * H + head];
+            beta = cur.b;
         } else {
-            dec = load4(static_cast<const float *>(a.gate) + base + 4 * kc);
-            beta = static_cast<const float *>(a.beta)[static_cast<int64_t>(t) * H + head];
+            dec = cur.g;
+            beta = cur.b;
         }
         if (norm) {
             // x / sqrt(sum x^2 + 1e-6), eps inside the sqrt; q then scaled.
@@ -216,6 +248,9 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
         if (kc < NP) {
             store1(op + base + row0 + kc * RPP, mine);
         }
+        if (more) {
+            cur = nxt;
+        }
     }
 
     // Tokens no sequence covers are zero (the reference allocates
@@ -246,7 +281,9 @@ template <int D, typename TQK, typename TV, int GATE>
 KernelFn pick_np(int np) {
     if constexpr (D == 128) {
         switch (np) {
+            case 8: return recurrent_kernel<D, 8, TQK, TV, GATE>;
             case 4: return recurrent_kernel<D, 4, TQK, TV, GATE>;
+            case 2: return recurrent_kernel<D, 2, TQK, TV, GATE>;
             case 1: return recurrent_kernel<D, 1, TQK, TV, GATE>;
             default: return nullptr;
         }
@@ -345,14 +382,26 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
     if (kargs.head_count == 0 || kargs.head_begin + kargs.head_count > kargs.num_heads) {
         kargs.head_count = kargs.num_heads - kargs.head_begin;
     }
-    // V-split: four workgroups per (sequence, head) at D=128 (32 value rows,
-    // 16 KB of state each). At B=256, H=32 this streams the state at 5.9 TB/s
-    // against 5.75 TB/s with two 64-row workgroups and 5.6 TB/s with eight
-    // 16-row ones; 8-row tiles only for small batches.
+    // V-split at D=128, by tokens per sequence (measured on MI355X): one token
+    // (decode) -> 16-row tiles, eight workgroups per (sequence, head): 6.3 TB/s
+    // at B=256, H=32 against 6.05 with 32-row tiles; two tokens -> 32-row
+    // tiles; more (verify, recurrent prefill) -> 64-row tiles, which spread
+    // the per-token work (token loads, norms, reductions) over more rows
+    // (4 tokens x 1024 sequences, H=16: 456 us against 498 with 32-row tiles).
+    // Small batches use 8-row tiles so the launch still fills the GPU.
     const int64_t pairs = static_cast<int64_t>(a.num_seqs) * kargs.head_count;
     int np;
     if (D == 128) {
-        np = pairs >= 128 ? 4 : 1;
+        const int64_t tokens = a.num_tokens;
+        if (pairs < 128) {
+            np = 1;
+        } else if (tokens <= a.num_seqs) {
+            np = 2;
+        } else if (tokens <= 2 * static_cast<int64_t>(a.num_seqs)) {
+            np = 4;
+        } else {
+            np = 8;
+        }
     } else {
         np = pairs >= 2048 ? 4 : 1;
     }

@@ -12,10 +12,12 @@ sequences by one token in place). ``value`` = tokens/s = 256 / step time.
 Also reported (same JSON line): the chunked prefill of ``configs[2]`` (T=8192
 single sequence, H=32, K=V=128, chunk 64) as ``prefill``, the decode kernel's
 roofline (algorithmic bytes / kernel time, measured with HIP events on the
-launch stream), and the CPU baseline (this repository's torch oracle of the
-reference CPU path, on the host cores, over a bounded sample).
+launch stream), ``more_configs`` (configs 4 and 5 prefill and config 5's
+4-token decode, a few timed calls each, inputs drawn on the device) and the CPU
+baseline (this repository's torch oracle of the reference CPU path, on the
+host cores, over a bounded sample).
 
-Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]``.
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-more]``.
 """
 
 from __future__ import annotations
@@ -53,10 +55,10 @@ DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
 # The kernel-trace/PMC summaries are kept under profiles/.
 FETCH_SCALE = 524288.0 / 262156.8
 WRITE_SCALE = 524288.0 / 524288.0
-DEC_FETCH_KIB, DEC_WRITE_KIB = 267456.0, 526342.9
+DEC_FETCH_KIB, DEC_WRITE_KIB = 267451.4, 526336.2
 DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
-PF_TRAFFIC = ((180759.8 + 276671.1) * FETCH_SCALE + (526336.1 + 79101.2) * WRITE_SCALE) * 1024
+PF_TRAFFIC = ((180780.2 + 276925.4) * FETCH_SCALE + (526336.2 + 78994.4) * WRITE_SCALE) * 1024
 
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
@@ -152,6 +154,118 @@ def run_prefill(steps, warmup, device="cuda"):
     return dict(ms_per_step=ms_step, gpu_us=gpu_us)
 
 
+# Configs 4 and 5 (reported beside the headline, a few timed calls each).
+BYTES_PER_TOKEN_ROW = 3 * 128 * 2 + 128 * 4 + 4 + 128 * 2  # q,k,v bf16, g fp32, beta, o bf16
+FLOP_PER_TOKEN_HEAD = 2 * (5 * 64 * 128 + 3 * 128 * 128)
+
+
+def _device_case(heads, lengths, *, slots, indices, seed, gate=(1.0, 0.0), zero_pool=False,
+                 device="cuda"):
+    """BASELINE-config distributions drawn on the device (the large configs would
+    take seconds to draw on the host): q, k L2-normalized bf16, v bf16,
+    ``g = logsigmoid(randn*gate[0] + gate[1])`` fp32, ``beta = sigmoid(randn)``
+    fp32, pool ``randn*0.05`` (or zeros) K-contiguous."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    T = int(sum(lengths))
+    D = 128
+
+    def l2(x):
+        return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=gen, device=device)
+
+    q = l2(rnd(1, T, heads, D)).bfloat16()
+    k = l2(rnd(1, T, heads, D)).bfloat16()
+    v = rnd(1, T, heads, D).bfloat16()
+    g = torch.nn.functional.logsigmoid(rnd(1, T, heads, D) * gate[0] + gate[1])
+    beta = torch.sigmoid(rnd(1, T, heads))
+    if zero_pool:
+        pool = torch.zeros(slots, heads, D, D, device=device).transpose(-1, -2)
+    else:
+        pool = (rnd(slots, heads, D, D) * 0.05).transpose(-1, -2)
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + int(n))
+    return dict(q=q, k=k, v=v, g=g, beta=beta, pool=pool,
+                idx=torch.tensor(list(indices), dtype=torch.int32, device=device),
+                cu=torch.tensor(cu, dtype=torch.int32, device=device), scale=D ** -0.5)
+
+
+def _time(step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) * 1e3 / steps
+
+
+def run_more(steps=5, warmup=1):
+    """Configs 4 and 5 prefill, and config 5's 4-token decode, on the device."""
+    from tests import kda_cases as C
+
+    ops = torch.ops.sgl_glm53_ascend
+    out = {}
+
+    def prefill(name, heads, lengths, slots, indices, seed, gate, zero_pool):
+        c = _device_case(heads, lengths, slots=slots, indices=indices, seed=seed, gate=gate,
+                         zero_pool=zero_pool)
+        T = int(sum(lengths))
+        N = len(lengths)
+
+        def step():
+            return ops.kda_prepared_varlen_chunk(
+                c["q"], c["k"], c["v"], c["g"], c["beta"], initial_state_source=c["pool"],
+                initial_state_indices=c["idx"], cu_seqlens=c["cu"], scale=c["scale"])
+
+        us = _time(step, steps, warmup)
+        flop = T * heads * FLOP_PER_TOKEN_HEAD
+        state_bytes = N * heads * 128 * 128 * 4 * (1 if zero_pool else 2)
+        nbytes = T * heads * BYTES_PER_TOKEN_ROW + state_bytes
+        tf = flop / (us * 1e-6) / 1e12
+        out[name] = dict(tokens=T, heads=heads, seqs=N, gpu_us=us, tok_per_s=T / (us * 1e-6),
+                         tflops=tf, mfma_frac=tf / BF16_PEAK_TFLOPS,
+                         attainable_frac=(tf * 1e12) / min(BF16_PEAK_TFLOPS * 1e12,
+                                                           HBM_PEAK_GBS * 1e9 * flop / nbytes),
+                         algorithmic_flop=flop, algorithmic_bytes=nbytes)
+        _log(f"{name}: {us:.1f} us, {tf:.1f} TFLOP/s")
+        del c
+
+    g4 = C.gen(4)
+    lengths4 = [int(x) for x in torch.randint(1, 4097, (16,), generator=g4)]
+    idx4 = torch.randperm(64, generator=g4)[:16].tolist()
+    prefill("config4_prefill", 32, lengths4, 64, idx4, 4, (1.0, 0.0), False)
+    prefill("config5_prefill", 16, [65536], 2, [1], 5, (2.0, -2.0), True)
+
+    # config 5 decode: 1024 sequences x 4 tokens from a 2048-slot pool, harsh decay
+    n5, steps5, h5, slots5 = 1024, 4, 16, 2048
+    idx5 = torch.randperm(slots5, generator=C.gen(5))[:n5].tolist()
+    c = _device_case(h5, [steps5] * n5, slots=slots5, indices=idx5, seed=55, gate=(2.0, -2.0))
+
+    def dstep():
+        return ops.kda_prepared_varlen_recurrent(
+            c["q"], c["k"], c["v"], c["g"], c["beta"], initial_state_source=c["pool"],
+            initial_state_indices=c["idx"], cu_seqlens=c["cu"], scale=c["scale"])
+
+    us = _time(dstep, max(steps, 10), max(warmup, 2))
+    nbytes = (n5 * h5 * 2 * 128 * 128 * 4 + n5 * steps5 * h5 * BYTES_PER_TOKEN_ROW
+              + (n5 + 1) * 4 + n5 * 4)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out["config5_decode"] = dict(seqs=n5, tokens_per_seq=steps5, heads=h5, pool_slots=slots5,
+                                 kernel_us=us, tok_per_s=n5 * steps5 / (us * 1e-6),
+                                 hbm_gbs=gbs, hbm_frac=gbs / HBM_PEAK_GBS,
+                                 algorithmic_bytes=nbytes)
+    _log(f"config5_decode: {us:.1f} us, {gbs:.0f} GB/s")
+    return out
+
+
 def cpu_baseline(budget_s=10.0):
     """The oracle's recurrent decode (the reference CPU path's loop structure,
     bench/kda_chunk/kda_python.py:253-307) on the host cores."""
@@ -195,6 +309,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workload")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode workload")
+    ap.add_argument("--no-more", action="store_true",
+                    help="skip the config 4 / 5 lines reported beside the headline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (the known-size kernel "
                          "the FETCH_SIZE / WRITE_SIZE counters are scaled by), then exit")
@@ -250,6 +366,10 @@ def main():
             )
             _log(f"prefill: {pf['ms_per_step']*1e3:.1f} us/step, {tf:.1f} TFLOP/s")
 
+    more = None
+    if not args.no_more:
+        more = run_more()
+
     cpu = None
     if not args.no_cpu:
         _log("cpu baseline: oracle decode on host cores")
@@ -279,10 +399,11 @@ def main():
         roofline=dict(
             bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
             frac=achieved / HBM_PEAK_GBS, traffic=DEC_TRAFFIC,
-            kernel="recurrent_kernel<128,4,bf16,bf16,LOG>",
+            kernel="recurrent_kernel<128,2,bf16,bf16,LOG>",
             algorithmic_bytes_per_launch=DEC_BYTES, kernel_us=dec["kernel_us"],
         ),
         prefill=prefill,
+        more_configs=more,
         cpu_baseline=cpu,
     )
     print(json.dumps(line), flush=True)

@@ -349,3 +349,56 @@ def test_c_abi_launch_direct(gpu_ops):
     ref = _oracle_prepared(case, ref_pool)
     C.assert_out(out.cpu(), ref, C.OUT_TOL, "output")
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "state")
+
+
+def test_config5_decode_full_size(gpu_ops):
+    """BASELINE config 5's decode half at full size: 1024 sequences x 4 tokens,
+    H=16, harsh decay, 2048-slot pool. Sequences are independent, so a seeded
+    sample of 12 is checked against the oracle from their own initial slots;
+    every slot no sequence indexes must come back bit-identical."""
+    n, steps, heads, slots, D = 1024, 4, 16, 2048, 128
+    dev = "cuda"
+    gen = torch.Generator(device=dev).manual_seed(55)
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=gen, device=dev)
+
+    def l2(x):
+        return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+
+    T = n * steps
+    q = l2(rnd(1, T, heads, D)).bfloat16()
+    k = l2(rnd(1, T, heads, D)).bfloat16()
+    v = rnd(1, T, heads, D).bfloat16()
+    g = torch.nn.functional.logsigmoid(rnd(1, T, heads, D) * 2.0 - 2.0)
+    beta = torch.sigmoid(rnd(1, T, heads))
+    pool = (rnd(slots, heads, D, D) * 0.05).transpose(-1, -2)
+    perm = torch.randperm(slots, generator=C.gen(5))[:n]
+    idx = perm.to(torch.int32).to(dev)
+    cu = C.cu_from_lengths([steps] * n).to(dev)
+    sample = torch.randperm(n, generator=C.gen(6))[:12].tolist()
+    before = {s: pool[int(perm[s])].cpu().clone() for s in sample}
+    untouched = torch.ones(slots, dtype=torch.bool)
+    untouched[perm] = False
+    untouched_idx = untouched.nonzero().flatten().to(dev)
+    untouched_before = pool.index_select(0, untouched_idx).clone()
+
+    out = gpu_ops.kda_prepared_varlen_recurrent(q, k, v, g, beta, initial_state_source=pool,
+                                                initial_state_indices=idx, cu_seqlens=cu,
+                                                scale=D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.index_select(0, untouched_idx), untouched_before)
+    e_o = e_s = 0.0
+    for s in sample:
+        rows = slice(s * steps, (s + 1) * steps)
+        ref_pool = torch.zeros(2, heads, D, D)
+        ref_pool[1] = before[s]  # the sequence's own slot as slot 1
+        ref = R.kda_recurrent(q[:, rows].float().cpu() * D ** -0.5, k[:, rows].float().cpu(),
+                              v[:, rows].float().cpu(), g[:, rows].cpu(), beta[:, rows].cpu(),
+                              state_pool=ref_pool, state_indices=torch.tensor([1], dtype=torch.int32),
+                              cu_seqlens=torch.tensor([0, steps], dtype=torch.int32),
+                              out_dtype=torch.float32)
+        e_o = max(e_o, C.assert_out(out[:, rows].cpu(), ref, C.OUT_TOL, f"sequence {s} output"))
+        e_s = max(e_s, C.assert_rel(pool[int(perm[s])].cpu(), ref_pool[1], C.STATE_TOL,
+                                    f"sequence {s} state"))
+    print(f"config5 decode: output err {e_o:.2e}, state err {e_s:.2e}")
