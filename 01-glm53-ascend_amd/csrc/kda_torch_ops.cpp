@@ -25,6 +25,7 @@
 // never has to be read back.
 
 #include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
@@ -38,6 +39,10 @@
 namespace {
 
 using NamedTensor = std::pair<const char *, const at::Tensor &>;
+
+void check_same_device(const at::Tensor &q, const char *name, const at::Tensor &t) {
+    TORCH_CHECK(t.device() == q.device(), name, " must be on the same device as q");
+}
 
 void check_ok(int status, const char *op) {
     TORCH_CHECK(status == KDA_OK, op, ": ", kda_status_string(status), " (status ", status, ")");
@@ -56,6 +61,28 @@ std::optional<at::Tensor> as_int32_opt(const std::optional<at::Tensor> &t) {
 }
 
 const int32_t *i32_ptr(const at::Tensor &t) { return t.data_ptr<int32_t>(); }
+
+// One packed token batch [1, T, H, D] (the sglang contract; a leading batch
+// above one would otherwise be ignored), with T and the request count in the
+// kernels' int32 range.
+void check_packed(const char *op, const at::Tensor &q, const at::Tensor &indices) {
+    TORCH_CHECK(q.size(0) == 1, op, " expects one packed token batch [1, T, H, D], got batch ",
+                q.size(0));
+    TORCH_CHECK(q.size(1) <= INT32_MAX && indices.numel() < INT32_MAX, op,
+                " supports at most 2^31-1 tokens and requests");
+}
+
+void check_gate_params(const at::Tensor &q, const at::Tensor &A_log, const at::Tensor &dt_bias,
+                       int64_t HV, int64_t D) {
+    TORCH_CHECK(A_log.scalar_type() == at::kFloat && A_log.numel() == HV,
+                "A_log must be fp32 with HV elements");
+    TORCH_CHECK(dt_bias.scalar_type() == at::kFloat && dt_bias.numel() == HV * D,
+                "dt_bias must be fp32 with HV*K elements");
+    TORCH_CHECK(A_log.is_contiguous() && dt_bias.is_contiguous(),
+                "A_log and dt_bias must be contiguous");
+    check_same_device(q, "A_log", A_log);
+    check_same_device(q, "dt_bias", dt_bias);
+}
 
 void check_index_tensors(const char *op, const at::Tensor &q, const at::Tensor &indices,
                          const at::Tensor &cu_seqlens) {
@@ -111,10 +138,6 @@ void check_on_gpu(const char *name, const at::Tensor &t) {
     TORCH_CHECK(t.device().is_cuda(), name, " must be a CUDA (HIP) tensor");
 }
 
-void check_same_device(const at::Tensor &q, const char *name, const at::Tensor &t) {
-    TORCH_CHECK(t.device() == q.device(), name, " must be on the same device as q");
-}
-
 struct PoolRef {
     float *base;
     int64_t stride_slot;
@@ -140,6 +163,7 @@ at::Tensor varlen_recurrent_impl(const char *op, const at::Tensor &A_log, const 
                                  const std::optional<at::Tensor> &track_lens) {
     TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, op,
                 " expects q, k, v as [1, T, H, D]");
+    check_packed(op, q, indices);
     const int64_t H = k.size(2);
     const int64_t D = k.size(3);
     const int64_t HV = v.size(2);
@@ -159,12 +183,7 @@ at::Tensor varlen_recurrent_impl(const char *op, const at::Tensor &A_log, const 
     TORCH_CHECK(q.sizes() == k.sizes() && a.sizes() == k.sizes() && v.size(1) == q.size(1),
                 op, " expects q, k, a as [1, T, H, K] and v as [1, T, H, V]");
     TORCH_CHECK(b.numel() == q.size(1) * H, op, " expects b as [1, T, H]");
-    TORCH_CHECK(A_log.scalar_type() == at::kFloat && A_log.numel() == HV,
-                "A_log must be fp32 with HV elements");
-    TORCH_CHECK(dt_bias.scalar_type() == at::kFloat && dt_bias.numel() == HV * D,
-                "dt_bias must be fp32 with HV*K elements");
-    check_same_device(q, "A_log", A_log);
-    check_same_device(q, "dt_bias", dt_bias);
+    check_gate_params(q, A_log, dt_bias, HV, D);
     check_pool(pool, HV, D);
     check_same_device(q, "initial_state_source", pool);
     if (save_mid) {
@@ -202,6 +221,7 @@ at::Tensor varlen_recurrent_impl(const char *op, const at::Tensor &A_log, const 
     }
 
     check_on_gpu("q", q);
+    const c10::DeviceGuard device_guard(q.device());  // launch on q's device
     const at::Tensor idx32 = as_int32(indices);
     const at::Tensor cu32 = as_int32(cu_seqlens);
     const auto ti32 = as_int32_opt(track_indices);
@@ -313,6 +333,7 @@ at::Tensor varlen_chunk_impl(const char *op, const at::Tensor &A_log, const at::
                              const std::optional<at::Tensor> &track_lens) {
     TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, op,
                 " expects q, k, v as [1, T, H, D]");
+    check_packed(op, q, indices);
     const int64_t H = k.size(2);
     const int64_t D = k.size(3);
     const int64_t HV = v.size(2);
@@ -328,12 +349,7 @@ at::Tensor varlen_chunk_impl(const char *op, const at::Tensor &A_log, const at::
     TORCH_CHECK(q.sizes() == k.sizes() && a.sizes() == k.sizes() && v.size(1) == q.size(1),
                 op, " expects q, k, a as [1, T, H, K] and v as [1, T, H, V]");
     TORCH_CHECK(b.numel() == q.size(1) * H, op, " expects b as [1, T, H]");
-    TORCH_CHECK(A_log.scalar_type() == at::kFloat && A_log.numel() == HV,
-                "A_log must be fp32 with HV elements");
-    TORCH_CHECK(dt_bias.scalar_type() == at::kFloat && dt_bias.numel() == HV * D,
-                "dt_bias must be fp32 with HV*K elements");
-    check_same_device(q, "A_log", A_log);
-    check_same_device(q, "dt_bias", dt_bias);
+    check_gate_params(q, A_log, dt_bias, HV, D);
     check_pool(pool, HV, D);
     check_same_device(q, "initial_state_source", pool);
     check_index_tensors(op, q, indices, cu_seqlens);
@@ -342,6 +358,7 @@ at::Tensor varlen_chunk_impl(const char *op, const at::Tensor &A_log, const at::
     const int64_t T = q.size(1);
     const int64_t N = indices.numel();
     check_on_gpu("q", q);
+    const c10::DeviceGuard device_guard(q.device());  // launch on q's device
     const at::Tensor idx32 = as_int32(indices);
     const at::Tensor cu32 = as_int32(cu_seqlens);
     const auto ti32 = as_int32_opt(track_indices);
@@ -431,6 +448,7 @@ PreparedInputs check_prepared(const char *op, const at::Tensor &q, const at::Ten
                               bool allow_d64) {
     TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4 && g.dim() == 4, op,
                 " expects q, k, v, g as [1, T, H, D]");
+    check_packed(op, q, indices);
     const auto dt = q.scalar_type();
     TORCH_CHECK(dt == at::kBFloat16 || dt == at::kFloat, op, ": q must be bf16 or fp32");
     for (const auto &named : {NamedTensor{"q", q}, NamedTensor{"k", k}, NamedTensor{"v", v}}) {
@@ -487,6 +505,7 @@ at::Tensor kda_prepared_varlen_recurrent(const at::Tensor &q, const at::Tensor &
                     mid.size(0), " for ", N, " requests");
     }
     check_on_gpu("q", q);
+    const c10::DeviceGuard device_guard(q.device());  // launch on q's device
     const at::Tensor idx32 = as_int32(initial_state_indices);
     const at::Tensor cu32 = as_int32(cu_seqlens);
     const auto ti32 = as_int32_opt(track_state_indices);
@@ -552,6 +571,7 @@ at::Tensor kda_prepared_varlen_chunk(const at::Tensor &q, const at::Tensor &k,
     TORCH_CHECK(p.qk_dtype == KDA_BF16, op, " takes bf16 q, k, v (bf16 MFMA operands)");
     const int64_t N = initial_state_indices.numel();
     check_on_gpu("q", q);
+    const c10::DeviceGuard device_guard(q.device());  // launch on q's device
     const at::Tensor idx32 = as_int32(initial_state_indices);
     const at::Tensor cu32 = as_int32(cu_seqlens);
     const auto ti32 = as_int32_opt(track_state_indices);
@@ -626,12 +646,20 @@ void prepared_recurrent(const at::Tensor &qn, const at::Tensor &kn, const at::Te
                     (v.scalar_type() == at::kBFloat16 || v.scalar_type() == at::kFloat),
                 "v and out must share a bf16 or fp32 dtype");
     TORCH_CHECK(v.is_contiguous() && out.is_contiguous(), "v and out must be contiguous");
+    for (const auto &named : {NamedTensor{"v", v}, NamedTensor{"out", out},
+                              NamedTensor{"beta", beta}, NamedTensor{"state", state},
+                              NamedTensor{"indices", indices}, NamedTensor{"starts", starts}}) {
+        TORCH_CHECK(named.second.device() == qn.device(), named.first,
+                    " must be on the same device as qn");
+    }
     const int64_t rows = qn.numel() / D;
     TORCH_CHECK(rows % H == 0 && kn.numel() == qn.numel() && v.numel() == qn.numel() &&
                     gdecay.numel() == qn.numel() && out.numel() == qn.numel() &&
                     beta.numel() == rows,
                 op, ": qn, kn, v, gdecay, out must hold T*H rows of D, beta T*H values");
     const int64_t T = rows / H;
+    TORCH_CHECK(T <= INT32_MAX && starts.numel() <= INT32_MAX, op,
+                " supports at most 2^31-1 tokens and requests");
     TORCH_CHECK(starts.scalar_type() == at::kInt || starts.scalar_type() == at::kLong,
                 "starts must be int32 or int64");
     TORCH_CHECK(indices.scalar_type() == at::kInt || indices.scalar_type() == at::kLong,
@@ -658,6 +686,7 @@ void prepared_recurrent(const at::Tensor &qn, const at::Tensor &kn, const at::Te
     check_on_gpu("qn", qn);
     check_on_gpu("kn", kn);
     check_on_gpu("v", v);
+    const c10::DeviceGuard device_guard(qn.device());  // launch on qn's device
     if (N == 0 || T == 0) {
         return;
     }

@@ -301,6 +301,43 @@ def cpu_baseline(budget_s=10.0):
     )
 
 
+def cpu_baseline_prefill(budget_s=12.0):
+    """The oracle's chunked prefill (the reference CPU path's structure,
+    bench/kda_chunk/kda_python.py:41-188) on the host cores, over a bounded
+    sample of config 3: the first 512 of its 8192 tokens, all 32 heads."""
+    from oracle import kda_ref as R
+    from tests import kda_cases as C
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    sample_t = 512
+    case = C.prepared_case(PF_H, (sample_t,), D=PF_D, slots=2, indices=[1], seed=3,
+                           zero_pool=True)
+    qs = case.q.float() * case.scale
+
+    def once():
+        pool = C.clone_pool(case.pool)
+        t0 = time.perf_counter()
+        R.kda_chunk(qs, case.k, case.v, case.g, case.beta, state_pool=pool,
+                    state_indices=case.indices, cu_seqlens=case.cu_seqlens)
+        return time.perf_counter() - t0
+
+    once()  # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 20):
+        times.append(once())
+    med = statistics.median(times)
+    return dict(
+        value=sample_t / med,
+        unit="tok/s",
+        cores=torch.get_num_threads(),
+        kind="port",
+        sample=(f"oracle kda_chunk (torch fp32, CPU, chunk 64) on the first {sample_t} of the "
+                f"8192 config-3 tokens, H={PF_H}, K=V={PF_D}; median of {len(times)} runs; "
+                f"os.cpu_count()={os.cpu_count()}"),
+    )
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -375,6 +412,10 @@ def main():
         _log("cpu baseline: oracle decode on host cores")
         cpu = cpu_baseline()
         _log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+        if prefill is not None:
+            _log("cpu baseline: oracle chunked prefill on host cores")
+            prefill["cpu_baseline"] = cpu_baseline_prefill()
+            _log(f"cpu baseline (prefill): {prefill['cpu_baseline']['value']:.1f} tok/s")
 
     line = dict(
         metric="KDA decode tok/s + state HBM GB/s (B=256); chunk prefill tok/s (T=8k)",

@@ -198,3 +198,20 @@ def test_prepared_recurrent_validates():
     with pytest.raises(RuntimeError, match="track_indices is required"):
         prepared_recurrent(qn, qn, v, qn, torch.zeros(T * H), out, state, idx, starts,
                            track_state=True)
+
+
+@pytest.mark.parametrize("op", [kda_varlen_recurrent, kda_varlen_chunk])
+def test_rejects_batched_tokens(op):
+    case = _case(lengths=(1, 1), prefill=op is kda_varlen_chunk)
+    for n in ("q", "k", "v", "a"):
+        case[n] = torch.cat([case[n], case[n]])  # [2, T, H, D]
+    case["b"] = torch.cat([case["b"], case["b"]])
+    with pytest.raises(RuntimeError, match="expects one packed token batch"):
+        op(**case)
+
+
+def test_rejects_strided_gate_params():
+    case = _case()
+    case["dt_bias"] = torch.zeros(2 * 4 * D)[::2]
+    with pytest.raises(RuntimeError, match="A_log and dt_bias must be contiguous"):
+        kda_varlen_recurrent(**case)
