@@ -22,7 +22,7 @@
 //                           factors e^(<=0)), the blocked triangular inverse in
 //                           fp32, w and u on MFMA; writes the scan's operands as
 //                           ready MFMA fragments;
-//   K2 chunk_scan_kernel    one workgroup per (sequence, head, 16 value
+//   K2 chunk_scan_kernel    one workgroup per (sequence, head, 16 or 32 value
 //                           columns), the serial chunk recurrence: four chain
 //                           waves carry S (fp32, registers) and vnew, four
 //                           output waves compute o one phase behind; S and
@@ -47,6 +47,8 @@
 // of slice s.
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 
 #include "kda_abi.h"
 #include "kda_device.h"
@@ -887,13 +889,13 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 }
 
 // ---------------------------------------------------------------------------
-// K2: the serial chunk scan per (sequence, head, 16 value columns).
+// K2: the serial chunk scan per (sequence, head, CW = 16 NT value columns).
 //
 // Eight waves in two roles, so every SIMD holds two independent instruction
 // streams:
-//   chain waves 0-3  own S rows [32c, 32c+32) (fp32, registers) and run the
-//                    recurrence: publish S_j, vnew_j = u - w S_j, publish
-//                    vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j;
+//   chain waves 0-3  own S rows [32c, 32c+32) x CW columns (fp32, registers)
+//                    and run the recurrence: publish S_j, vnew_j = u - w S_j,
+//                    publish vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j;
 //   output waves 4-7 own token rows [16o, 16o+16) and compute
 //                    o_j = (q e^G) S_j + Aqk vnew_j one phase behind the chain.
 // Per chunk j there are two workgroup barriers: B1(j) after S_j is published,
@@ -901,25 +903,33 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 // by j's parity. Output waves compute (q e^G) S_j between B2(j) and B1(j+1)
 // (while the chain runs its state update) and add Aqk vnew_j between B1(j+1)
 // and B2(j+1); buffer j&1 is rewritten only at chunk j+2, after both.
+//
+// The chunk operands (w, kd, q e^G, Aqk: ~96 KiB per chunk) are the same for
+// every column group of a (sequence, head), so a wider group (NT = 2) reads
+// fewer operand bytes per unit of work; a narrower one (NT = 1) has the
+// shorter serial step. The host picks NT from the number of chains.
 // ---------------------------------------------------------------------------
 
 constexpr int kScanThreads = 512;
 
+template <int NT>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws) {
-    __shared__ u32x4 sbuf[2][4][2][64];         // S_j as B fragments: [parity][slice][hi, lo][lane]
-    __shared__ uint32_t vbuf[2][2][2][64][4];   // vnew_j as B fragments: [parity][slice][hi, lo]
-    __shared__ uint32_t otile[4][16][8];        // per output wave: 16 rows x 16 bf16 columns
+    constexpr int NV = 8 / NT;  // column groups per (sequence, head)
+    constexpr int CW = 16 * NT;
+    __shared__ u32x4 sbuf[2][4][2][NT][64];         // S_j as B fragments: [parity][slice][hi, lo][tile][lane]
+    __shared__ uint32_t vbuf[2][2][2][NT][64][4];   // vnew_j as B fragments: [parity][slice][hi, lo][tile]
+    __shared__ uint32_t otile[4][16][CW / 2];       // per output wave: 16 rows x CW bf16 columns
 
     const int H = a.num_heads;
     const int N = a.num_seqs;
     const int pairs = N * H;
-    // XCD-aware order: the 8 column tiles of one (sequence, head) share an XCD
-    // (and its L2), since they read the same chunk records.
+    // XCD-aware order: the NV column groups of one (sequence, head) share an
+    // XCD (and its L2), since they read the same chunk records.
     const int b = blockIdx.x;
     const int xcd = b & 7;
     const int rest = b >> 3;
-    const int vt = rest & 7;
-    const int pair = (rest >> 3) * 8 + xcd;
+    const int vt = rest % NV;
+    const int pair = (rest / NV) * 8 + xcd;
     if (pair >= pairs) {
         return;
     }
@@ -940,7 +950,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     const int wr = w & 3;
     const int r = lane & 15;
     const int gq = lane >> 4;
-    const int vcol = 16 * vt + r;
+    const int col0 = CW * vt;  // first value column of this group
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
     uint16_t *out = static_cast<uint16_t *>(a.out);
     auto rec_of = [&](int j) {
@@ -964,27 +974,35 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
         }
         const int64_t head_off = static_cast<int64_t>(h) * a.state_stride_head;
+        // state element (row 16 kt + 4 gq + i, column col0 + 16 ct + r) of slot s
+        auto state_ptr = [&](int s, int tt, int ct) {
+            return a.state + s * a.state_stride_slot + head_off +
+                   static_cast<int64_t>(col0 + 16 * ct + r) * DK + 16 * (2 * wr + tt) + 4 * gq;
+        };
 
-        // S rows [32wr, 32wr+32): tiles kt = 2wr + tt, lane holds S[16kt + 4gq + i][vcol].
-        f32x4 S[2];
+        // S rows [32wr, 32wr+32): tiles (kt = 2wr + tt, ct), lane holds
+        // S[16kt + 4gq + i][col0 + 16ct + r].
+        f32x4 S[2][NT];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            if (slot > 0) {
-                const float *src = a.state + slot * a.state_stride_slot + head_off +
-                                   static_cast<int64_t>(vcol) * DK + 16 * (2 * wr + tt) + 4 * gq;
-                const float4 s4 = load4(src);
-                S[tt] = f32x4{s4.x, s4.y, s4.z, s4.w};
-            } else {
-                S[tt] = z4;
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) {
+                if (slot > 0) {
+                    const float4 s4 = load4(state_ptr(slot, tt, ct));
+                    S[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
+                } else {
+                    S[tt][ct] = z4;
+                }
             }
         }
-        auto store_S = [&](int dst_slot, const f32x4 *val) {
+        auto store_S = [&](int dst_slot, const f32x4 (&val)[2][NT]) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                float *dst = a.state + dst_slot * a.state_stride_slot + head_off +
-                             static_cast<int64_t>(vcol) * DK + 16 * (2 * wr + tt) + 4 * gq;
-                *reinterpret_cast<float4 *>(dst) =
-                    make_float4(val[tt][0], val[tt][1], val[tt][2], val[tt][3]);
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    *reinterpret_cast<float4 *>(state_ptr(dst_slot, tt, ct)) =
+                        make_float4(val[tt][ct][0], val[tt][ct][1], val[tt][ct][2], val[tt][ct][3]);
+                }
             }
         };
         if (track_slot > 0 && track_len == 0) {
@@ -996,7 +1014,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // fragments are in flight while this chunk computes.
         struct Ops {
             bf16x8 Wf[4], Kh[2][2], Kl[2][2];
-            f32x4 u, gl[2];
+            f32x4 u[NT], gl[2];
         };
         auto load_ops = [&](Ops &op, int j) {
             const char *rec = rec_of(j);
@@ -1012,7 +1030,10 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                     op.Kl[tt][s] = load_frag(rec, kOffKdL, (2 * wr + tt) * 2 + s, lane);
                 }
             }
-            op.u = reinterpret_cast<const f32x4 *>(rec + kOffU)[(wr * 8 + vt) * 64 + lane];
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) {
+                op.u[ct] = reinterpret_cast<const f32x4 *>(rec + kOffU)[(wr * 8 + NT * vt + ct) * 64 + lane];
+            }
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 op.gl[tt] = *reinterpret_cast<const f32x4 *>(rec + kOffGl +
@@ -1024,96 +1045,113 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             const int p = j & 1;
             const int len = eos - (bos + BT * j) < BT ? eos - (bos + BT * j) : BT;
             // A. publish S_j (slice wr) as hi/lo B fragments
-            {
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) {
                 float x[8];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    x[i] = S[0][i];
-                    x[4 + i] = S[1][i];
+                    x[i] = S[0][ct][i];
+                    x[4 + i] = S[1][ct][i];
                 }
                 bf16x8 hi, lo;
                 split_bf16x8(x, hi, lo);
-                sbuf[p][wr][0][lane] = as_u32x4(hi);
-                sbuf[p][wr][1][lane] = as_u32x4(lo);
+                sbuf[p][wr][0][ct][lane] = as_u32x4(hi);
+                sbuf[p][wr][1][ct][lane] = as_u32x4(lo);
             }
             lds_barrier();  // B1(j)
-            // B. vnew rows [16wr, 16wr+16) = u - w S_j (single pass), published hi/lo
-            {
+            // B. vnew rows [16wr, 16wr+16) = u - w S_j (single pass), published hi/lo;
+            // tile mt = wr is half wr%2 of slice wr/2
+            const int sl = wr >> 1;
+            const int hf = (wr & 1) * 2;
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) {
                 f32x4 acc = z4;
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    acc = mfma(op.Wf[s], as_bf16x8(sbuf[p][s][0][lane]), acc);
+                    acc = mfma(op.Wf[s], as_bf16x8(sbuf[p][s][0][ct][lane]), acc);
                 }
                 uint32_t hp[2], lp[2];
 #pragma unroll
                 for (int q2 = 0; q2 < 2; ++q2) {
-                    const float v0 = op.u[2 * q2] - acc[2 * q2];
-                    const float v1 = op.u[2 * q2 + 1] - acc[2 * q2 + 1];
+                    const float v0 = op.u[ct][2 * q2] - acc[2 * q2];
+                    const float v1 = op.u[ct][2 * q2 + 1] - acc[2 * q2 + 1];
                     hp[q2] = pack_bf16x2(v0, v1);
                     lp[q2] = pack_bf16x2(v0 - __uint_as_float(hp[q2] << 16),
                                          v1 - __uint_as_float(hp[q2] & 0xffff0000u));
                 }
-                // tile mt = wr is half wr%2 of slice wr/2
-                const int sl = wr >> 1;
-                const int hf = (wr & 1) * 2;
-                vbuf[p][sl][0][lane][hf] = hp[0];
-                vbuf[p][sl][0][lane][hf + 1] = hp[1];
-                vbuf[p][sl][1][lane][hf] = lp[0];
-                vbuf[p][sl][1][lane][hf + 1] = lp[1];
+                vbuf[p][sl][0][ct][lane][hf] = hp[0];
+                vbuf[p][sl][0][ct][lane][hf + 1] = hp[1];
+                vbuf[p][sl][1][ct][lane][hf] = lp[0];
+                vbuf[p][sl][1][ct][lane][hf + 1] = lp[1];
             }
             lds_barrier();  // B2(j)
             // C. S_{j+1} = e^(G_last) S_j + kd^T vnew_j (3-pass)
-            bf16x8 vh[2], vl[2];
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                vh[s] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][lane][0]));
-                vl[s] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][lane][0]));
-            }
+            auto vfrag = [&](int s, int hl, int ct) {
+                return as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][hl][ct][lane][0]));
+            };
             // tracked prefix strictly inside this chunk
             const int rr = track_len - BT * j;
             if (track_slot > 0 && rr > 0 && rr < len) {
-                f32x4 St[2];
+                f32x4 St[2][NT];
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
                     const f32x4 g2 = *reinterpret_cast<const f32x4 *>(
                         tr + kTrOffGl + 4 * (16 * (2 * wr + tt) + 4 * gq));
-                    f32x4 tu = z4;
+                    bf16x8 th[2], tl[2];
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
-                        const bf16x8 th = load_frag(tr, kTrOffKdH, (2 * wr + tt) * 2 + s, lane);
-                        const bf16x8 tl = load_frag(tr, kTrOffKdL, (2 * wr + tt) * 2 + s, lane);
-                        tu = mfma(th, vh[s], tu);
-                        tu = mfma(th, vl[s], tu);
-                        tu = mfma(tl, vh[s], tu);
+                        th[s] = load_frag(tr, kTrOffKdH, (2 * wr + tt) * 2 + s, lane);
+                        tl[s] = load_frag(tr, kTrOffKdL, (2 * wr + tt) * 2 + s, lane);
                     }
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        St[tt][i] = S[tt][i] * g2[i] + tu[i];
+                    for (int ct = 0; ct < NT; ++ct) {
+                        f32x4 tu = z4;
+#pragma unroll
+                        for (int s = 0; s < 2; ++s) {
+                            const bf16x8 vh = vfrag(s, 0, ct);
+                            const bf16x8 vl = vfrag(s, 1, ct);
+                            tu = mfma(th[s], vh, tu);
+                            tu = mfma(th[s], vl, tu);
+                            tu = mfma(tl[s], vh, tu);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            St[tt][ct][i] = S[tt][ct][i] * g2[i] + tu[i];
+                        }
                     }
                 }
                 store_S(track_slot, St);
             }
-            f32x4 su[2] = {z4, z4};
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
+            for (int ct = 0; ct < NT; ++ct) {
+                bf16x8 vh[2], vl[2];
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    su[tt] = mfma(op.Kh[tt][s], vh[s], su[tt]);
+                for (int s = 0; s < 2; ++s) {
+                    vh[s] = vfrag(s, 0, ct);
+                    vl[s] = vfrag(s, 1, ct);
+                }
+                f32x4 su[2] = {z4, z4};
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        su[tt] = mfma(op.Kh[tt][s], vh[s], su[tt]);
+                    }
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        su[tt] = mfma(op.Kh[tt][s], vl[s], su[tt]);
+                    }
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        su[tt] = mfma(op.Kl[tt][s], vh[s], su[tt]);
+                    }
                 }
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
-                    su[tt] = mfma(op.Kh[tt][s], vl[s], su[tt]);
-                }
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    su[tt] = mfma(op.Kl[tt][s], vh[s], su[tt]);
-                }
-            }
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    S[tt][i] = S[tt][i] * op.gl[tt][i] + su[tt][i];
+                    for (int i = 0; i < 4; ++i) {
+                        S[tt][ct][i] = S[tt][ct][i] * op.gl[tt][i] + su[tt][i];
+                    }
                 }
             }
             if (track_slot > 0 && rr == len) {
@@ -1157,53 +1195,76 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 op.Al[s] = load_frag(rec, kOffAqL, wr * 2 + s, lane);
             }
         };
-        f32x4 P = z4;  // (q e^G) S of the chunk whose output is pending
+        f32x4 P[NT];  // (q e^G) S of the chunk whose output is pending
+#pragma unroll
+        for (int ct = 0; ct < NT; ++ct) {
+            P[ct] = z4;
+        }
         // o_j = P + Aqk vnew_j (3-pass); rows t < len of chunk j are stored,
-        // transposed through this wave's LDS tile so each lane writes 4
-        // consecutive columns of one row (one 8-byte nontemporal store).
+        // transposed through this wave's LDS tile so each lane writes CW/4
+        // consecutive columns of one row (nontemporal stores).
         auto finish = [&](const OpsO &op, int j) {
             const int p = j & 1;
-            f32x4 acc = P;
+            uint16_t *ot = reinterpret_cast<uint16_t *>(&otile[wr][0][0]);
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][lane][0]));
-                const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][lane][0]));
-                acc = mfma(op.Ah[s], vh, acc);
-                acc = mfma(op.Ah[s], vl, acc);
-                acc = mfma(op.Al[s], vh, acc);
+            for (int ct = 0; ct < NT; ++ct) {
+                f32x4 acc = P[ct];
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][ct][lane][0]));
+                    const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][ct][lane][0]));
+                    acc = mfma(op.Ah[s], vh, acc);
+                    acc = mfma(op.Ah[s], vl, acc);
+                    acc = mfma(op.Al[s], vh, acc);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    ot[(4 * gq + i) * CW + 16 * ct + r] = f32_to_bf16(acc[i]);
+                }
             }
             const int t0 = bos + BT * j;
             const int len = eos - t0 < BT ? eos - t0 : BT;
-            uint16_t *ot = reinterpret_cast<uint16_t *>(&otile[wr][0][0]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ot[(4 * gq + i) * 16 + r] = f32_to_bf16(acc[i]);
-            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             const int row = lane >> 2;
             const int cq = lane & 3;
-            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-            const u32x2 val = *reinterpret_cast<const u32x2 *>(&otile[wr][row][2 * cq]);
             const int t = 16 * wr + row;
-            if (t < len) {
-                __builtin_nontemporal_store(
-                    val, reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(t0 + t) * H + h) * DK +
-                                                   16 * vt + 4 * cq));
+            uint16_t *dst = out + (static_cast<int64_t>(t0 + t) * H + h) * DK + col0 + cq * (CW / 4);
+            if constexpr (NT == 1) {
+                typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 val = *reinterpret_cast<const u32x2 *>(&otile[wr][row][2 * cq]);
+                if (t < len) {
+                    __builtin_nontemporal_store(val, reinterpret_cast<u32x2 *>(dst));
+                }
+            } else {
+                u32x4 val[NT / 2];
+#pragma unroll
+                for (int k = 0; k < NT / 2; ++k) {
+                    val[k] = *reinterpret_cast<const u32x4 *>(&otile[wr][row][(CW / 8) * cq + 4 * k]);
+                }
+                if (t < len) {
+#pragma unroll
+                    for (int k = 0; k < NT / 2; ++k) {
+                        __builtin_nontemporal_store(val[k], reinterpret_cast<u32x4 *>(dst) + k);
+                    }
+                }
             }
         };
         // P = (q e^G) S_j (3-pass), rows [16wr, 16wr+16)
         auto start = [&](const OpsO &op, int j) {
             const int p = j & 1;
-            f32x4 acc = z4;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const bf16x8 sh = as_bf16x8(sbuf[p][s][0][lane]);
-                const bf16x8 sl = as_bf16x8(sbuf[p][s][1][lane]);
-                acc = mfma(op.Qh[s], sh, acc);
-                acc = mfma(op.Qh[s], sl, acc);
-                acc = mfma(op.Ql[s], sh, acc);
+            for (int ct = 0; ct < NT; ++ct) {
+                f32x4 acc = z4;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const bf16x8 sh = as_bf16x8(sbuf[p][s][0][ct][lane]);
+                    const bf16x8 sl = as_bf16x8(sbuf[p][s][1][ct][lane]);
+                    acc = mfma(op.Qh[s], sh, acc);
+                    acc = mfma(op.Qh[s], sl, acc);
+                    acc = mfma(op.Ql[s], sh, acc);
+                }
+                P[ct] = acc;
             }
-            P = acc;
         };
         // Iteration j: [B1(j)] finish chunk j-1 (operands in `other`), load
         // chunk j+1 into `other`, [B2(j)] start chunk j (operands in `cur`).
@@ -1223,31 +1284,48 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         if (nch > 0) {
             load_out(opA, 0);
         }
-        // L2 warm-up: at chunk j each workgroup reads one dword of its
-        // eighth of the 1028 cache lines of chunk j + kWarmAhead's record, so
-        // the record is in L2 before its eight column tiles load it. Each
-        // value is folded in two chunks later, when the loads issued after it
-        // have been waited for anyway.
+        // L2 warm-up: at chunk j each workgroup reads one dword of each line of
+        // its 1/NV share of chunk j + kWarmAhead's record (1028 cache lines), so
+        // the record is in L2 before the column groups load it. Each value is
+        // folded in two chunks later, when the loads issued after it have been
+        // waited for anyway.
         constexpr int kWarmAhead = 3;
-        uint32_t warm = 0, wa = 0, wb = 0;
-        auto touch = [&](int jj) {
-            int l = vt * 129 + wr * 32 + (lane & 31);
-            l = l < kRecBytes / 128 - 1 ? l : kRecBytes / 128 - 1;
-            return *reinterpret_cast<const uint32_t *>(rec_of(jj < nch ? jj : nch - 1) + l * 128);
+        constexpr int kLines = kRecBytes / 128;
+        constexpr int kShare = (kLines + NV - 1) / NV;
+        constexpr int kTouch = (kShare + 255) / 256;  // lines per output lane
+        uint32_t warm = 0, wa[kTouch], wb[kTouch];
+#pragma unroll
+        for (int k = 0; k < kTouch; ++k) {
+            wa[k] = 0;
+            wb[k] = 0;
+        }
+        auto touch = [&](uint32_t (&dst)[kTouch], int jj) {
+            const char *rec = rec_of(jj < nch ? jj : nch - 1);
+#pragma unroll
+            for (int k = 0; k < kTouch; ++k) {
+                warm ^= dst[k];
+                int i = k * 256 + wr * 64 + lane;
+                i = i < kShare ? i : kShare - 1;
+                int l = vt * kShare + i;
+                l = l < kLines - 1 ? l : kLines - 1;
+                dst[k] = *reinterpret_cast<const uint32_t *>(rec + l * 128);
+            }
         };
         for (int j = 0; j < nch; j += 2) {
-            warm ^= wa;
-            wa = touch(j + kWarmAhead);
+            touch(wa, j + kWarmAhead);
             iter(opA, opB, j);
             if (j + 1 >= nch) {
                 break;
             }
-            warm ^= wb;
-            wb = touch(j + 1 + kWarmAhead);
+            touch(wb, j + 1 + kWarmAhead);
             iter(opB, opA, j + 1);
         }
+#pragma unroll
+        for (int k = 0; k < kTouch; ++k) {
+            warm ^= wa[k] ^ wb[k];
+        }
         // keeps the warm-up loads (never true: num_tokens >= 0)
-        if ((warm ^ wa ^ wb) == 0x9e3779b9u && a.num_tokens < 0) {
+        if (warm == 0x9e3779b9u && a.num_tokens < 0) {
             out[0] = 0;
         }
     }
@@ -1256,9 +1334,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     auto zero_rows = [&](int ta, int tb) {
         for (int t = ta + tid / 16; t < tb; t += kScanThreads / 16) {
             if ((tid & 15) == 0) {
-                // one thread per token row writes this tile's 16 columns
-                for (int cidx = 0; cidx < 16; ++cidx) {
-                    out[(static_cast<int64_t>(t) * H + h) * DK + 16 * vt + cidx] = 0;
+                // one thread per token row writes this group's CW columns
+                for (int cidx = 0; cidx < CW; ++cidx) {
+                    out[(static_cast<int64_t>(t) * H + h) * DK + col0 + cidx] = 0;
                 }
             }
         }
@@ -1272,6 +1350,39 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 }
 
 bool aligned(const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; }
+
+// Compute units of the current device, queried once per device.
+int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        return 256;
+    }
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            n = 256;
+        }
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Value tiles per scan workgroup for `pairs` (sequence, head) chains. A
+// 16-column group has the shortest chunk step (≈1.5 µs on config 3 and 5) but
+// each of its workgroups reads the whole chunk record for 16 columns; a
+// 32-column group takes ≈2.1 µs per step for twice the columns. So the narrow
+// groups win while all of them run at once (pairs x 8 <= CUs), the wide ones
+// as soon as the narrow ones would need a second round (config 4: 847 -> 652
+// µs for the scan).
+int scan_tiles(int64_t pairs) { return pairs * 8 <= device_cus() ? 1 : 2; }
+
+const void *scan_kernel(int nt) {
+    return nt == 2 ? reinterpret_cast<const void *>(chunk_scan_kernel<2>)
+                   : reinterpret_cast<const void *>(chunk_scan_kernel<1>);
+}
+
+int64_t scan_blocks(int64_t pairs, int nt) { return (pairs + 7) / 8 * 8 * (8 / nt); }
 
 }  // namespace chunk
 }  // namespace kda
@@ -1349,13 +1460,14 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     }
     {
         const int64_t pairs = static_cast<int64_t>(a.num_seqs) * a.num_heads;
-        const int64_t blocks = (pairs + 7) / 8 * 64;
+        const int nt = scan_tiles(pairs);
+        const int64_t blocks = scan_blocks(pairs, nt);
         if (blocks > 0x7fffffff) {
             return KDA_ERR_INVALID_ARGUMENT;
         }
         const char *cws = ws;
         void *params[] = {&kargs, &cws};
-        if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_scan_kernel),
+        if (hipLaunchKernel(scan_kernel(nt),
                             dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads), params, 0,
                             st) != hipSuccess) {
             return KDA_ERR_LAUNCH;

@@ -57,6 +57,9 @@ REF_CASES = [
     ("unaligned varlen", 3, (1, 37, 100, 64, 130), [1, 2, 3, 0, 5], None),
     ("track in ragged tail", 2, (100, 37), [1, 2], ([6, 0], [90, 3])),
     ("track end of ragged", 2, (100,), [1], ([6], [100])),
+    # more than 32 (sequence, head) chains: the scan runs 32-column groups
+    ("wide groups varlen", 40, (130, 64, 37), [1, 2, 3], ([4, 0, 5], [100, 0, 20])),
+    ("wide groups zero slot", 33, (70,), [0], None),
 ]
 
 
@@ -95,11 +98,11 @@ def test_chunk_index_dtypes_bit_identical(gpu_ops):
     assert torch.equal(pool.cpu(), base_pool.cpu())
 
 
-def test_chunk_tokens_outside_sequences_are_zero(gpu_ops):
-    case = C.raw_case(2, (70, 30), slots=4, seed=8)
+@pytest.mark.parametrize("heads", [2, 40])
+def test_chunk_tokens_outside_sequences_are_zero(gpu_ops, heads):
+    case = C.raw_case(heads, (70, 30), slots=4, seed=8)
     T = case.q.shape[1]
     case.cu_seqlens = torch.tensor([0, 70, T - 5], dtype=torch.int32)
-    torch.full((1, T, 2, 128), float("nan"), device=DEV, dtype=torch.bfloat16)
     out, _ = _run_chunk(gpu_ops, case)
     out = out.cpu()
     assert torch.equal(out[0, T - 5:], torch.zeros_like(out[0, T - 5:]))
