@@ -142,11 +142,8 @@ __device__ __forceinline__ void split_bf16x8(const float x[8], bf16x8 &hi, bf16x
     lo = as_bf16x8(l);
 }
 
-// Record stores are nontemporal: a record is read back only by the scan, long
-// after, so it need not occupy L2 meanwhile (the prepare kernel's own input
-// loads then see less contention: -7% on config 3).
 __device__ __forceinline__ void store_frag(char *base, int off, int idx, int lane, bf16x8 v) {
-    __builtin_nontemporal_store(as_u32x4(v), reinterpret_cast<u32x4 *>(base + off) + idx * 64 + lane);
+    reinterpret_cast<u32x4 *>(base + off)[idx * 64 + lane] = as_u32x4(v);
 }
 __device__ __forceinline__ bf16x8 load_frag(const char *base, int off, int idx, int lane) {
     return as_bf16x8(reinterpret_cast<const u32x4 *>(base + off)[idx * 64 + lane]);
@@ -276,9 +273,13 @@ template <int GATE>
 __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkArgs a, char *ws,
                                                                  int nrec) {
     __shared__ PrepShared sm;
-    const int c = blockIdx.x;
-    const int h = blockIdx.y;
+    // Workgroups run chunk-descending, heads fastest: the scan starts with the
+    // first chunk of every sequence and head, so those records are written
+    // last and are still in the memory-side cache when it reads them (plain
+    // write-back stores; with this order they beat nontemporal ones by 2%).
     const int H = a.num_heads;
+    const int c = (nrec - 1) - static_cast<int>(blockIdx.x) / H;
+    const int h = static_cast<int>(blockIdx.x) % H;
     const int N = a.num_seqs;
     const Layout LY = layout(a.num_tokens, N, H);
     const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
@@ -311,9 +312,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     const uint16_t *qp = static_cast<const uint16_t *>(a.q);
 
     // S3 work units: (row block I, channel half sh = slices 2sh and 2sh+1),
-    // each with its pairs (I, J <= I); the two halves of every product meet
-    // in LDS through float atomics. Five half-pairs and two half-blocks per
-    // wave:  wave 0: (3,0) (0,0)   wave 1: (3,1) (0,1)
+    // each with its pairs (I, J <= I); the two halves of every product are
+    // summed through LDS (half 1 stores, half 0 adds after a barrier). Five
+    // half-pairs and two half-blocks per wave:  wave 0: (3,0) (0,0)   wave 1: (3,1) (0,1)
     //        wave 2: (2,0) (1,0)   wave 3: (2,1) (1,1)
     const int sh = wave & 1;
     const int IA = wave < 2 ? 3 : 2;
@@ -859,7 +860,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 acc = mfma(Th[s], vb, acc);
                 acc = mfma(Tl[s], vb, acc);
             }
-            __builtin_nontemporal_store(acc, reinterpret_cast<f32x4 *>(rec + kOffU) + (wave * 8 + vt) * 64 + lane);
+            reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = acc;
         }
         // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k (K = token), B = T^T
 #pragma unroll
@@ -1453,7 +1454,11 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
                              : reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_LOG>);
         int nr = nrec;
         void *params[] = {&kargs, &ws, &nr};
-        if (hipLaunchKernel(fn, dim3(static_cast<unsigned>(nrec), static_cast<unsigned>(a.num_heads)),
+        const int64_t prep_blocks = static_cast<int64_t>(nrec) * a.num_heads;
+        if (prep_blocks > 0x7fffffff) {
+            return KDA_ERR_INVALID_ARGUMENT;
+        }
+        if (hipLaunchKernel(fn, dim3(static_cast<unsigned>(prep_blocks)),
                             dim3(kThreads), params, 0, st) != hipSuccess) {
             return KDA_ERR_LAUNCH;
         }

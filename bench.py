@@ -338,11 +338,18 @@ def cpu_baseline_prefill(budget_s=12.0):
     )
 
 
+def _prefill_steps(args):
+    """(steps, warmup) for the config-3 prefill: half the decode step count and
+    the decode's warm-up (10 calls by default: the first few dozen calls on a
+    fresh box run 10-20% slow while clocks and address translation settle)."""
+    return max(3, args.steps // 2), max(1, args.warmup)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workload")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode workload")
@@ -372,7 +379,7 @@ def main():
     if args.no_decode:
         # profiling aid: the prefill workload alone (no JSON line)
         _log("prefill: config 3 (T=8192, H=32, K=V=128, chunk 64)")
-        pf = run_prefill(max(3, args.steps // 5), max(1, args.warmup // 5))
+        pf = run_prefill(*_prefill_steps(args))
         if pf is not None:
             _log(f"prefill: {pf['ms_per_step']*1e3:.1f} us/step")
         return
@@ -386,7 +393,7 @@ def main():
     prefill = None
     if not args.no_prefill:
         _log("prefill: config 3 (T=8192, H=32, K=V=128, chunk 64)")
-        pf = run_prefill(max(3, args.steps // 5), max(1, args.warmup // 5))
+        pf = run_prefill(*_prefill_steps(args))
         if pf is not None:
             tf = PF_FLOP / (pf["gpu_us"] * 1e-6) / 1e12
             prefill = dict(
@@ -405,7 +412,7 @@ def main():
 
     more = None
     if not args.no_more:
-        more = run_more()
+        more = run_more(max(3, args.steps // 5), max(1, args.warmup))
 
     cpu = None
     if not args.no_cpu:
