@@ -55,10 +55,10 @@ DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
 # The kernel-trace/PMC summaries are kept under profiles/.
 FETCH_SCALE = 524288.0 / 262156.8
 WRITE_SCALE = 524288.0 / 524288.0
-DEC_FETCH_KIB, DEC_WRITE_KIB = 267452.0, 526336.2
+DEC_FETCH_KIB, DEC_WRITE_KIB = 267451.4, 526336.1
 DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
-PF_TRAFFIC = ((180040.3 + 307650.1) * FETCH_SCALE + (526394.5 + 74686.3) * WRITE_SCALE) * 1024
+PF_TRAFFIC = ((168226.2 + 343399.2) * FETCH_SCALE + (526336.0 + 94244.6) * WRITE_SCALE) * 1024
 
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
