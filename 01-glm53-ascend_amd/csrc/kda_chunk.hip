@@ -70,13 +70,13 @@ constexpr int kFrag = 1024;
 constexpr int kOffW = 0;                          // w hi: A (mt 0..3, s 0..3)
 constexpr int kOffQgH = kOffW + 16 * kFrag;       // q e^G hi: A (mt, s)
 constexpr int kOffQgL = kOffQgH + 16 * kFrag;     // q e^G lo
-constexpr int kOffAqH = kOffQgL + 16 * kFrag;     // Aqk hi: A (mt 0..3, s 0..1)
-constexpr int kOffAqL = kOffAqH + 8 * kFrag;      // Aqk lo
-constexpr int kOffKdH = kOffAqL + 8 * kFrag;      // kd^T hi: A (mk 0..7, s 0..1)
+constexpr int kOffAqH = kOffQgL + 16 * kFrag;     // Aqk hi: A (mt, s), see aq_frag
+constexpr int kOffAqL = kOffAqH + 6 * kFrag;      // Aqk lo
+constexpr int kOffKdH = kOffAqL + 6 * kFrag;      // kd^T hi: A (mk 0..7, s 0..1)
 constexpr int kOffKdL = kOffKdH + 16 * kFrag;     // kd^T lo
 constexpr int kOffU = kOffKdL + 16 * kFrag;       // u fp32: C (mt 0..3, vt 0..7)
 constexpr int kOffGl = kOffU + 32 * kFrag;        // e^(G_last) fp32 [128]
-constexpr int kRecBytes = kOffGl + DK * 4;        // 131584
+constexpr int kRecBytes = kOffGl + DK * 4;        // 127488
 // Track record of one (sequence, head): operands of the state after r < len
 // tokens of the chunk holding the tracked position.
 constexpr int kTrOffKdH = 0;
@@ -95,6 +95,10 @@ struct Layout {
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 __host__ __device__ inline int max_chunks(int T, int N) { return (T + BT - 1) / BT + N; }
+
+// Aqk is lower triangular: its fragments (mt, s = 1) for mt < 2 (rows < 32,
+// columns >= 32) are zero and not stored, leaving six per record.
+__host__ __device__ constexpr int aq_frag(int mt, int s) { return mt < 2 ? mt : 2 * mt - 2 + s; }
 
 __host__ __device__ inline Layout layout(int T, int N, int H) {
     Layout L;
@@ -733,6 +737,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         const int row = 16 * wave + r;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
+            if (s == 1 && wave < 2) {
+                break;  // an all-zero fragment (uniform per wave)
+            }
             const float4 x0 = *reinterpret_cast<const float4 *>(&sm.LT[row][32 * s + 4 * gq]);
             const float4 x1 = *reinterpret_cast<const float4 *>(&sm.LT[row][32 * s + 16 + 4 * gq]);
             const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -743,8 +750,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             }
             bf16x8 fh, fl;
             split_bf16x8(x, fh, fl);
-            store_frag(rec, kOffAqH, wave * 2 + s, lane, fh);
-            store_frag(rec, kOffAqL, wave * 2 + s, lane, fl);
+            store_frag(rec, kOffAqH, aq_frag(wave, s), lane, fh);
+            store_frag(rec, kOffAqL, aq_frag(wave, s), lane, fl);
         }
     }
 
@@ -1190,10 +1197,12 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 op.Qh[s] = load_frag(rec, kOffQgH, wr * 4 + s, lane);
                 op.Ql[s] = load_frag(rec, kOffQgL, wr * 4 + s, lane);
             }
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                op.Ah[s] = load_frag(rec, kOffAqH, wr * 2 + s, lane);
-                op.Al[s] = load_frag(rec, kOffAqL, wr * 2 + s, lane);
+            // rows [16wr, 16wr+16) meet columns >= 32 only for wr >= 2
+            op.Ah[0] = load_frag(rec, kOffAqH, aq_frag(wr, 0), lane);
+            op.Al[0] = load_frag(rec, kOffAqL, aq_frag(wr, 0), lane);
+            if (wr >= 2) {
+                op.Ah[1] = load_frag(rec, kOffAqH, aq_frag(wr, 1), lane);
+                op.Al[1] = load_frag(rec, kOffAqL, aq_frag(wr, 1), lane);
             }
         };
         f32x4 P[NT];  // (q e^G) S of the chunk whose output is pending
@@ -1212,6 +1221,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 f32x4 acc = P[ct];
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
+                    if (s == 1 && wr < 2) {
+                        break;  // Aqk is zero there (uniform per wave)
+                    }
                     const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][ct][lane][0]));
                     const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][ct][lane][0]));
                     acc = mfma(op.Ah[s], vh, acc);
@@ -1286,7 +1298,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             load_out(opA, 0);
         }
         // L2 warm-up: at chunk j each workgroup reads one dword of each line of
-        // its 1/NV share of chunk j + kWarmAhead's record (1028 cache lines), so
+        // its 1/NV share of chunk j + kWarmAhead's record (996 cache lines), so
         // the record is in L2 before the column groups load it. Each value is
         // folded in two chunks later, when the loads issued after it have been
         // waited for anyway.
