@@ -1364,11 +1364,17 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 
 bool aligned(const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; }
 
-// Compute units of the current device, queried once per device.
-int device_cus() {
+// Compute units of the device `stream` runs on, queried once per device.
+int device_cus(hipStream_t stream) {
     static std::atomic<int> cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) {
+        (void)hipGetLastError();  // leave no error behind for the caller's own checks
+        if (hipGetDevice(&dev) != hipSuccess) {
+            return 256;
+        }
+    }
+    if (dev < 0 || dev >= 64) {
         return 256;
     }
     int n = cache[dev].load(std::memory_order_relaxed);
@@ -1388,7 +1394,7 @@ int device_cus() {
 // groups win while all of them run at once (pairs x 8 <= CUs), the wide ones
 // as soon as the narrow ones would need a second round (config 4: 847 -> 652
 // µs for the scan).
-int scan_tiles(int64_t pairs) { return pairs * 8 <= device_cus() ? 1 : 2; }
+int scan_tiles(int64_t pairs, hipStream_t stream) { return pairs * 8 <= device_cus(stream) ? 1 : 2; }
 
 const void *scan_kernel(int nt) {
     return nt == 2 ? reinterpret_cast<const void *>(chunk_scan_kernel<2>)
@@ -1477,7 +1483,7 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     }
     {
         const int64_t pairs = static_cast<int64_t>(a.num_seqs) * a.num_heads;
-        const int nt = scan_tiles(pairs);
+        const int nt = scan_tiles(pairs, st);
         const int64_t blocks = scan_blocks(pairs, nt);
         if (blocks > 0x7fffffff) {
             return KDA_ERR_INVALID_ARGUMENT;
