@@ -3,7 +3,8 @@
 Each case draws a head count on either side of the chunk scan's 16/32-column
 switch (more than 32 (sequence, head) chains run 32-column scan groups on a
 256-CU part), 1-6 sequences whose lengths favour chunk boundaries (1, 63, 64,
-65, 127, 128, 129 tokens, or any length up to 300), state slots with the
+65, 127, 128, 129 tokens, or any length up to 300; in the prefill forms some
+sequences are empty), state slots with the
 padding slot 0 mixed in, and, for most cases, a tracked prefix per sequence
 into its own distinct slot (sometimes none, i.e. track slot 0). The chunk op is
 checked against ``oracle.kda_ref.kda_chunk`` and the recurrent op against
@@ -28,13 +29,13 @@ HEADS = (1, 2, 3, 5, 8, 17, 33, 40)
 LENGTHS = (1, 2, 63, 64, 65, 127, 128, 129)
 
 
-def _draw(seed, max_len=300, track_prob=0.6):
+def _draw(seed, max_len=300, track_prob=0.6, empty_prob=0.0):
     rng = random.Random(seed)
     heads = rng.choice(HEADS)
     n = rng.randint(1, 6)
     lengths = [rng.choice(LENGTHS) if rng.random() < 0.6 else rng.randint(1, max_len)
                for _ in range(n)]
-    lengths = [min(x, max_len) for x in lengths]
+    lengths = [0 if rng.random() < empty_prob else min(x, max_len) for x in lengths]
     slots = 2 * n + 2
     state_slots = rng.sample(range(1, slots), n)
     indices = [0 if rng.random() < 0.2 else s for s in state_slots]
@@ -61,7 +62,7 @@ def _prepared(case):
 
 @pytest.mark.parametrize("seed", range(16))
 def test_random_chunk_matches_oracle(gpu_ops, seed):
-    heads, lengths, slots, indices, track = _draw(1000 + seed)
+    heads, lengths, slots, indices, track = _draw(1000 + seed, empty_prob=0.1)
     label = f"seed {seed}: H={heads} lengths={lengths} indices={indices} track={track}"
     print(label, flush=True)
     case = C.raw_case(heads, lengths, indices=indices, slots=slots, seed=7000 + seed, track=track)
@@ -86,7 +87,8 @@ def test_random_recurrent_matches_oracle(gpu_ops, seed):
     prefill = seed % 2 == 0
     checkpoints = seed % 4 == 3
     heads, lengths, slots, indices, track = _draw(2000 + seed, max_len=8 if checkpoints else 300,
-                                                  track_prob=0.6 if prefill else 0.0)
+                                                  track_prob=0.6 if prefill else 0.0,
+                                                  empty_prob=0.1 if prefill else 0.0)
     label = (f"seed {seed}: H={heads} lengths={lengths} indices={indices} track={track} "
              f"prefill={prefill} checkpoints={checkpoints}")
     print(label, flush=True)
