@@ -55,10 +55,10 @@ DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
 # The kernel-trace/PMC summaries are kept under profiles/.
 FETCH_SCALE = 524288.0 / 262156.8
 WRITE_SCALE = 524288.0 / 524288.0
-DEC_FETCH_KIB, DEC_WRITE_KIB = 267451.4, 526336.1
+DEC_FETCH_KIB, DEC_WRITE_KIB = 267451.4, 526336.2
 DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
-PF_TRAFFIC = ((168226.2 + 343399.2) * FETCH_SCALE + (526336.0 + 94244.6) * WRITE_SCALE) * 1024
+PF_TRAFFIC = ((168219.6 + 261478.4) * FETCH_SCALE + (509952.0 + 108790.8) * WRITE_SCALE) * 1024
 
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
@@ -340,8 +340,9 @@ def cpu_baseline_prefill(budget_s=12.0):
 
 def _prefill_steps(args):
     """(steps, warmup) for the config-3 prefill: half the decode step count and
-    the decode's warm-up (10 calls by default: the first few dozen calls on a
-    fresh box run 10-20% slow while clocks and address translation settle)."""
+    the decode's warm-up count. On a fresh box the decode settles after ~150
+    calls (~25 ms: 188 -> 173 us per call) and the prefill after ~100 (~40 ms:
+    449 -> 381 us), hence the default of 200 warm-up calls."""
     return max(3, args.steps // 2), max(1, args.warmup)
 
 
@@ -349,7 +350,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workload")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode workload")
@@ -412,7 +413,7 @@ def main():
 
     more = None
     if not args.no_more:
-        more = run_more(max(3, args.steps // 5), max(1, args.warmup))
+        more = run_more(max(3, args.steps // 5), max(1, args.warmup // 4))
 
     cpu = None
     if not args.no_cpu:
