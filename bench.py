@@ -59,6 +59,11 @@ DEC_FETCH_KIB, DEC_WRITE_KIB = 267451.4, 526336.2
 DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
 PF_TRAFFIC = ((168219.6 + 261478.4) * FETCH_SCALE + (509952.0 + 108790.8) * WRITE_SCALE) * 1024
+# MFMA counters of the same two kernels (profiles/prefill_chunk_t8192_h32_mfma.md): matrix work
+# executed per call (SQ_INSTS_VALU_MFMA_MOPS_* x 512 FLOP; the hi/lo operand splits roughly
+# double the algorithmic count) and the fraction of SIMD cycles each kernel keeps the MFMA busy.
+PF_MFMA_EXECUTED_FLOP = (39845888 + 136314880 + 1048576) * 512
+PF_MFMA_BUSY = {"prepare": 28311552 / (3724619 / 8 * 1024), "scan": 68157440 / (3543351 / 8 * 1024)}
 
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
@@ -406,6 +411,8 @@ def main():
                 mfma_frac=tf / BF16_PEAK_TFLOPS,
                 hbm_gbs=PF_BYTES / (pf["gpu_us"] * 1e-6) / 1e9,
                 traffic=PF_TRAFFIC,
+                mfma_executed_tflops=PF_MFMA_EXECUTED_FLOP / (pf["gpu_us"] * 1e-6) / 1e12,
+                mfma_busy=PF_MFMA_BUSY,
                 attainable_frac=(tf * 1e12) / min(BF16_PEAK_TFLOPS * 1e12,
                                                   HBM_PEAK_GBS * 1e9 * PF_FLOP / PF_BYTES),
             )
