@@ -14,18 +14,25 @@
 //
 // MI355X mapping. The update never mixes value rows, so the state splits into
 // independent rows S[:, v], each a contiguous 4*D-byte line of the
-// K-contiguous pool. A lane owns four consecutive K elements (one 16-byte
-// vector) of NP rows; D/4 lanes span one row, so a wave-wide 16-byte load
-// covers 64/(D/4) complete rows -- fully coalesced 512 B (D=128) lines. The two
-// K-reductions per token (prediction and readout) are group sums over those
-// D/4 lanes (DPP + one ds_swizzle), so the state tile lives in VGPRs from the
-// first load to the single in-place write-back: HBM sees each state byte
-// exactly once in and once out. A workgroup (4 waves) covers NP*RPP value
-// rows of one (sequence, head); the host picks NP so small batches still
-// launch enough workgroups (V-split), large batches use one workgroup per
-// (sequence, head).
+// K-contiguous pool. A row is spread over L lanes (a row group); each lane
+// owns E = D/L of its K elements as E/4 16-byte vectors at K offsets
+// 4*kc + 4*L*j, so every wave-wide 16-byte load covers whole 4*L-element
+// segments of its rows -- complete cache lines. A lane holds the same K
+// elements of NP consecutive rows. The two K-reductions per token
+// (prediction and readout) are group sums over the L lanes (DPP, plus one
+// ds_swizzle when L = 32), so the state tile lives in VGPRs from the first
+// load to the single in-place write-back: HBM sees each state byte exactly
+// once in and once out. A workgroup (4 waves) covers 4*(64/L)*NP value rows
+// of one (sequence, head). The host picks the shape from the tokens per
+// sequence: one or two tokens (decode, short verify) use 32-lane rows, one
+// token with few rows per lane, so the launch has many small workgroups to
+// stream the state; three or more (verify, prefill) use 16-lane rows, whose
+// reductions take four DPP steps instead of five plus an LDS swizzle, with
+// four rows per lane to share each token's loads, exponentials and norms.
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "kda_abi.h"
 #include "kda_device.h"
@@ -35,15 +42,152 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <int D, int NP, typename TQK, typename TV, int GATE>
-__global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentArgs a) {
-    constexpr int L = D / 4;           // lanes per state row
-    constexpr int RPW = 64 / L;        // rows per wave per pass
-    constexpr int RPP = 4 * RPW;       // rows per workgroup per pass
-    constexpr int RB = NP * RPP;       // rows per workgroup
+// e^x as one v_exp_f32 of x*log2(e). The product's rounding puts the
+// relative error near |x| * 2^-24 plus the instruction's own ~1 ulp; a
+// result below the fp32 normal range may flush to zero.
+__device__ __forceinline__ float fexp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// Four consecutive K elements as loaded: 8 bytes of bf16 or 16 of fp32,
+// widened to fp32 at use.
+template <typename T> struct Raw4;
+template <> struct Raw4<uint16_t> {
+    uint2 r;
+    __device__ __forceinline__ void load(const uint16_t *p) {
+        r = *reinterpret_cast<const uint2 *>(p);
+    }
+    __device__ __forceinline__ float4 get() const {
+        return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                           __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+    }
+};
+template <> struct Raw4<float> {
+    float4 r;
+    __device__ __forceinline__ void load(const float *p) { r = *reinterpret_cast<const float4 *>(p); }
+    __device__ __forceinline__ float4 get() const { return r; }
+};
+
+// NP values of one token row (v in, o out), RS elements apart. Consecutive
+// ones (RS = 1) whose segment is aligned to its size (`vec`, up to 16
+// bytes) move in as few vector accesses as that allows; otherwise element
+// by element.
+template <typename T, int NP> struct RowVec {
+    float x[NP];
+    template <int RS>
+    __device__ __forceinline__ void load(const T *p, bool vec) {
+        if constexpr (RS == 1 && sizeof(T) == 2 && NP >= 2) {
+            if (vec) {
+                uint32_t w[NP / 2];
+                if constexpr (NP == 2) {
+                    w[0] = *reinterpret_cast<const uint32_t *>(p);
+                } else if constexpr (NP == 4) {
+                    const uint2 u = *reinterpret_cast<const uint2 *>(p);
+                    w[0] = u.x;
+                    w[1] = u.y;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < NP / 8; ++i) {
+                        const uint4 u = reinterpret_cast<const uint4 *>(p)[i];
+                        w[4 * i + 0] = u.x;
+                        w[4 * i + 1] = u.y;
+                        w[4 * i + 2] = u.z;
+                        w[4 * i + 3] = u.w;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < NP / 2; ++i) {
+                    x[2 * i] = __uint_as_float(w[i] << 16);
+                    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+                }
+                return;
+            }
+        } else if constexpr (RS == 1 && sizeof(T) == 4 && NP >= 4) {
+            if (vec) {
+#pragma unroll
+                for (int i = 0; i < NP / 4; ++i) {
+                    const float4 u = reinterpret_cast<const float4 *>(p)[i];
+                    x[4 * i + 0] = u.x;
+                    x[4 * i + 1] = u.y;
+                    x[4 * i + 2] = u.z;
+                    x[4 * i + 3] = u.w;
+                }
+                return;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            x[i] = load1(p + RS * i);
+        }
+    }
+    // Written by the row group's lanes kc: consecutive values by lane 0 as
+    // one vector when allowed, else value i by lane i (kc < NP).
+    template <int RS>
+    __device__ __forceinline__ void store_by(T *p, bool vec, int kc) const {
+        if constexpr (RS == 1 && sizeof(T) == 2 && NP >= 2) {
+            if (vec) {
+                if (kc != 0) {
+                    return;
+                }
+                uint32_t w[NP / 2];
+#pragma unroll
+                for (int i = 0; i < NP / 2; ++i) {
+                    w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+                }
+                if constexpr (NP == 2) {
+                    *reinterpret_cast<uint32_t *>(p) = w[0];
+                } else if constexpr (NP == 4) {
+                    *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < NP / 8; ++i) {
+                        reinterpret_cast<uint4 *>(p)[i] =
+                            make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+                    }
+                }
+                return;
+            }
+        } else if constexpr (RS == 1 && sizeof(T) == 4 && NP >= 4) {
+            if (vec) {
+                if (kc != 0) {
+                    return;
+                }
+#pragma unroll
+                for (int i = 0; i < NP / 4; ++i) {
+                    reinterpret_cast<float4 *>(p)[i] =
+                        make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+                }
+                return;
+            }
+        }
+        float mine = 0.f;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            mine = (kc == i) ? x[i] : mine;
+        }
+        if (kc < NP) {
+            store1(p + RS * kc, mine);
+        }
+    }
+};
+
+template <int D, int L, int NP, bool CONTIG, bool FEXP, typename TQK, typename TV, int GATE>
+__global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentArgs a, int vec_io) {
+    constexpr int E = D / L;           // K elements per lane
+    constexpr int EV = E / 4;          // 16-byte vectors per lane and row
+    constexpr int RPW = 64 / L;        // row groups per wave
+    constexpr int RPP = 4 * RPW;       // row groups per workgroup
+    constexpr int RB = RPP * NP;       // rows per workgroup
+    // A lane's NP rows: consecutive (CONTIG; v and o then move as one vector
+    // per row group) or RPP apart (each wave-wide state load then covers
+    // RPW adjacent rows, one contiguous span).
+    constexpr int RS = CONTIG ? 1 : RPP;
+    // The decay's exponential: one v_exp_f32 (FEXP) where the token loop's
+    // instruction count matters (several tokens per sequence), the correctly
+    // rounded expf where the launch is bound by the state traffic (decode).
+    auto dexp = [](float x) { return FEXP ? fexp(x) : expf(x); };
     constexpr int VT = D / RB;         // workgroups per (sequence, head)
-    static_assert(D % RB == 0, "a workgroup covers a whole number of row tiles");
-    static_assert(NP <= L, "one lane per row writes the output");
+    static_assert(E % 4 == 0 && D % RB == 0, "whole vectors and whole row tiles");
 
     const int H = a.num_heads;
     const int HC = a.head_count;  // heads in this launch, resolved by the host
@@ -62,9 +206,10 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int kc = lane % L;
-    const int rsub = lane / L;
-    const int row0 = vt * RB + wave * RPW + rsub;  // row of pass p: row0 + p*RPP
+    const int rgw = wave * RPW + lane / L;  // row group in the workgroup
+    const int row0 = vt * RB + (CONTIG ? rgw * NP : rgw);  // rows row0 + RS*p, p < NP
     const int T = a.num_tokens;
+    const bool vec = vec_io != 0;
 
     int bos = a.cu_seqlens[n];
     int eos = a.cu_seqlens[n + 1];
@@ -75,18 +220,26 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
         slot = 0;
     }
 
+    // Offset of this lane's vector j within a row of D elements.
+    auto koff = [&](int j) { return 4 * kc + 4 * L * j; };
     const int64_t head_off = static_cast<int64_t>(head) * a.state_stride_head;
-    float4 S[NP];
+    float4 S[NP][EV];
     if (slot > 0) {
         const float *src = a.state + slot * a.state_stride_slot + head_off;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            S[p] = load4_stream(src + static_cast<int64_t>(row0 + p * RPP) * D + 4 * kc);
+#pragma unroll
+            for (int j = 0; j < EV; ++j) {
+                S[p][j] = load4_stream(src + static_cast<int64_t>(row0 + RS * p) * D + koff(j));
+            }
         }
     } else {
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            S[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < EV; ++j) {
+                S[p][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
     }
 
@@ -108,7 +261,10 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     auto store_state = [&](float *dst) {
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            store4_stream(dst + static_cast<int64_t>(row0 + p * RPP) * D + 4 * kc, S[p]);
+#pragma unroll
+            for (int j = 0; j < EV; ++j) {
+                store4_stream(dst + static_cast<int64_t>(row0 + RS * p) * D + koff(j), S[p][j]);
+            }
         }
     };
     if (track_slot > 0 && track_len == 0) {
@@ -117,10 +273,17 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
 
     // Per-head gate constants (RAW): exp(A_log[h]) and this lane's dt_bias.
     float expA = 0.f;
-    float4 dtb = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 dtb[EV];
+#pragma unroll
+    for (int j = 0; j < EV; ++j) {
+        dtb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     if constexpr (GATE == KDA_GATE_RAW) {
         expA = expf(a.A_log[head]);
-        dtb = load4(a.dt_bias + static_cast<int64_t>(head) * D + 4 * kc);
+#pragma unroll
+        for (int j = 0; j < EV; ++j) {
+            dtb[j] = load4(a.dt_bias + static_cast<int64_t>(head) * D + koff(j));
+        }
     }
     const bool norm = (GATE == KDA_GATE_RAW) || (a.qk_l2norm != 0);
     const bool save_mid = a.intermediate != nullptr && slot > 0 && n < a.mid_rows;
@@ -129,138 +292,156 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     const TQK *kp = static_cast<const TQK *>(a.k);
     const TV *vp = static_cast<const TV *>(a.v);
     TV *op = static_cast<TV *>(a.out);
+    using TG = typename std::conditional<GATE == KDA_GATE_RAW, uint16_t, float>::type;
+    const TG *gp = static_cast<const TG *>(a.gate);
 
-    // One token's inputs, as loaded (gates are transformed at use). The next
-    // token's are loaded while the current one computes: a multi-token
+    // One token's inputs, as loaded (widened and transformed at use). The
+    // next token's are loaded while the current one computes: a multi-token
     // sequence (verify, prefill) would otherwise wait a full load latency per
-    // token. The branches on `more` are uniform across the workgroup.
+    // token. (Unrolling by two to alternate the buffers without copies costs
+    // more registers than the copies cost instructions.)
     struct TokenIn {
-        float4 q, k, g;
-        float v[NP];
+        Raw4<TQK> q[EV], k[EV];
+        Raw4<TG> g[EV];
+        RowVec<TV, NP> v;
         float b;
     };
     auto fetch = [&](int t, TokenIn &in) {
         const int64_t base = (static_cast<int64_t>(t) * H + head) * D;
-        in.q = load4(qp + base + 4 * kc);
-        in.k = load4(kp + base + 4 * kc);
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            in.v[p] = load1(vp + base + row0 + p * RPP);
+        for (int j = 0; j < EV; ++j) {
+            in.q[j].load(qp + base + koff(j));
+            in.k[j].load(kp + base + koff(j));
+            in.g[j].load(gp + base + koff(j));
         }
+        in.v.template load<RS>(vp + base + row0, vec);
         const int64_t bi = static_cast<int64_t>(t) * H + head;
         if constexpr (GATE == KDA_GATE_RAW) {
-            in.g = load4(static_cast<const uint16_t *>(a.gate) + base + 4 * kc);
             in.b = bf16_to_f32(static_cast<const uint16_t *>(a.beta)[bi]);
         } else {
-            in.g = load4(static_cast<const float *>(a.gate) + base + 4 * kc);
             in.b = static_cast<const float *>(a.beta)[bi];
         }
+    };
+    auto step = [&](const TokenIn &in, int t) {
+        float4 qv[EV], kv[EV], dec[EV];
+        float beta;
+#pragma unroll
+        for (int j = 0; j < EV; ++j) {
+            qv[j] = in.q[j].get();
+            kv[j] = in.k[j].get();
+            const float4 gv = in.g[j].get();
+            if constexpr (GATE == KDA_GATE_RAW) {
+                // g = lower_bound / (1 + exp(-(exp(A_log) * (a + dt_bias)))), decay = exp(g)
+                const float lb = a.lower_bound;
+                dec[j].x = dexp(lb / (1.0f + dexp(-(expA * (gv.x + dtb[j].x)))));
+                dec[j].y = dexp(lb / (1.0f + dexp(-(expA * (gv.y + dtb[j].y)))));
+                dec[j].z = dexp(lb / (1.0f + dexp(-(expA * (gv.z + dtb[j].z)))));
+                dec[j].w = dexp(lb / (1.0f + dexp(-(expA * (gv.w + dtb[j].w)))));
+            } else if constexpr (GATE == KDA_GATE_LOG) {
+                dec[j] = make_float4(dexp(gv.x), dexp(gv.y), dexp(gv.z), dexp(gv.w));
+            } else {
+                dec[j] = gv;
+            }
+        }
+        if constexpr (GATE == KDA_GATE_RAW) {
+            beta = 1.0f / (1.0f + dexp(-in.b));
+        } else {
+            beta = in.b;
+        }
+        float qsc = a.scale;
+        if (norm) {
+            // x / sqrt(sum x^2 + 1e-6), eps inside the sqrt; q then scaled.
+            float qs = 0.f, ks = 0.f;
+#pragma unroll
+            for (int j = 0; j < EV; ++j) {
+                qs += dot4(qv[j], qv[j]);
+                ks += dot4(kv[j], kv[j]);
+            }
+            qs = group_sum<L>(qs);
+            ks = group_sum<L>(ks);
+            const float kr = 1.0f / sqrtf(ks + 1e-6f);
+            qsc = (1.0f / sqrtf(qs + 1e-6f)) * a.scale;
+#pragma unroll
+            for (int j = 0; j < EV; ++j) {
+                kv[j] = make_float4(kv[j].x * kr, kv[j].y * kr, kv[j].z * kr, kv[j].w * kr);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < EV; ++j) {
+            qv[j] = make_float4(qv[j].x * qsc, qv[j].y * qsc, qv[j].z * qsc, qv[j].w * qsc);
+        }
+
+        float pred[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < EV; ++j) {
+                S[p][j].x *= dec[j].x;
+                S[p][j].y *= dec[j].y;
+                S[p][j].z *= dec[j].z;
+                S[p][j].w *= dec[j].w;
+                acc += dot4(S[p][j], kv[j]);
+            }
+            pred[p] = acc;
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            pred[p] = group_sum<L>(pred[p]);
+        }
+        RowVec<TV, NP> o;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float d = (in.v.x[p] - pred[p]) * beta;
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < EV; ++j) {
+                S[p][j].x += kv[j].x * d;
+                S[p][j].y += kv[j].y * d;
+                S[p][j].z += kv[j].z * d;
+                S[p][j].w += kv[j].w * d;
+                acc += dot4(S[p][j], qv[j]);
+            }
+            o.x[p] = acc;
+        }
+        const int step_i = t - bos;
+        if (save_mid && step_i < a.mid_steps) {
+            store_state(a.intermediate + n * a.mid_stride_req + step_i * a.mid_stride_step +
+                        static_cast<int64_t>(head) * a.mid_stride_head);
+        }
+        if (track_slot > 0 && step_i + 1 == track_len) {
+            store_state(a.state + track_slot * a.state_stride_slot + head_off);
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            o.x[p] = group_sum<L>(o.x[p]);
+        }
+        // every lane of the row group holds the sums
+        o.template store_by<RS>(op + (static_cast<int64_t>(t) * H + head) * D + row0, vec, kc);
     };
     TokenIn cur, nxt;
     if (bos < eos) {
         fetch(bos, cur);
     }
     for (int t = bos; t < eos; ++t) {
-        const bool more = t + 1 < eos;
-        if (more) {
+        if (t + 1 < eos) {
             fetch(t + 1, nxt);
         }
-        const int64_t base = (static_cast<int64_t>(t) * H + head) * D;
-        float4 qv = cur.q;
-        float4 kv = cur.k;
-        float vr[NP];
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            vr[p] = cur.v[p];
-        }
-        float4 dec;
-        float beta;
-        if constexpr (GATE == KDA_GATE_RAW) {
-            const float4 av = cur.g;
-            const float lb = a.lower_bound;
-            // g = lower_bound / (1 + exp(-(exp(A_log) * (a + dt_bias)))), decay = exp(g)
-            dec.x = expf(lb / (1.0f + expf(-(expA * (av.x + dtb.x)))));
-            dec.y = expf(lb / (1.0f + expf(-(expA * (av.y + dtb.y)))));
-            dec.z = expf(lb / (1.0f + expf(-(expA * (av.z + dtb.z)))));
-            dec.w = expf(lb / (1.0f + expf(-(expA * (av.w + dtb.w)))));
-            beta = 1.0f / (1.0f + expf(-cur.b));
-        } else if constexpr (GATE == KDA_GATE_LOG) {
-            const float4 gv = cur.g;
-            dec = make_float4(expf(gv.x), expf(gv.y), expf(gv.z), expf(gv.w));
-            beta = cur.b;
-        } else {
-            dec = cur.g;
-            beta = cur.b;
-        }
-        if (norm) {
-            // x / sqrt(sum x^2 + 1e-6), eps inside the sqrt; q then scaled.
-            const float qs = group_sum<L>(dot4(qv, qv));
-            const float ks = group_sum<L>(dot4(kv, kv));
-            const float qd = sqrtf(qs + 1e-6f);
-            const float kd = sqrtf(ks + 1e-6f);
-            qv = make_float4(qv.x / qd, qv.y / qd, qv.z / qd, qv.w / qd);
-            kv = make_float4(kv.x / kd, kv.y / kd, kv.z / kd, kv.w / kd);
-        }
-        const float sc = a.scale;
-        qv = make_float4(qv.x * sc, qv.y * sc, qv.z * sc, qv.w * sc);
-
-        float pred[NP];
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            S[p].x *= dec.x;
-            S[p].y *= dec.y;
-            S[p].z *= dec.z;
-            S[p].w *= dec.w;
-            pred[p] = dot4(S[p], kv);
-        }
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            pred[p] = group_sum<L>(pred[p]);
-        }
-        float o[NP];
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const float d = (vr[p] - pred[p]) * beta;
-            S[p].x += kv.x * d;
-            S[p].y += kv.y * d;
-            S[p].z += kv.z * d;
-            S[p].w += kv.w * d;
-            o[p] = dot4(S[p], qv);
-        }
-        const int step = t - bos;
-        if (save_mid && step < a.mid_steps) {
-            store_state(a.intermediate + n * a.mid_stride_req + step * a.mid_stride_step +
-                        static_cast<int64_t>(head) * a.mid_stride_head);
-        }
-        if (track_slot > 0 && step + 1 == track_len) {
-            store_state(a.state + track_slot * a.state_stride_slot + head_off);
-        }
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            o[p] = group_sum<L>(o[p]);
-        }
-        // Lane kc < NP writes row row0 + kc*RPP: one store per lane.
-        float mine = 0.f;
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            mine = (kc == p) ? o[p] : mine;
-        }
-        if (kc < NP) {
-            store1(op + base + row0 + kc * RPP, mine);
-        }
-        if (more) {
-            cur = nxt;
-        }
+        step(cur, t);
+        cur = nxt;
     }
 
     // Tokens no sequence covers are zero (the reference allocates
     // zeros_like(v), kda_varlen_recurrent.cpp:142): the first request zeroes
     // [0, cu[0]) and the last one [cu[N], T).
     auto zero_rows = [&](int t0, int t1) {
+        RowVec<TV, NP> z;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            z.x[p] = 0.f;
+        }
         for (int t = t0; t < t1; ++t) {
-            if (kc < NP) {
-                store1(op + (static_cast<int64_t>(t) * H + head) * D + row0 + kc * RPP, 0.f);
-            }
+            z.template store_by<RS>(op + (static_cast<int64_t>(t) * H + head) * D + row0, vec, kc);
         }
     };
     if (n == 0) {
@@ -275,50 +456,53 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     }
 }
 
-using KernelFn = void (*)(const KdaRecurrentArgs);
+using KernelFn = void (*)(const KdaRecurrentArgs, int);
+
+// Tile shapes: (lanes per row L, rows per lane NP).
+enum Shape { kDecode16, kDecode8, kMulti32, kMulti64, kD64Small, kD64Large };
 
 template <int D, typename TQK, typename TV, int GATE>
-KernelFn pick_np(int np) {
+KernelFn pick_shape(Shape shape) {
     if constexpr (D == 128) {
-        switch (np) {
-            case 8: return recurrent_kernel<D, 8, TQK, TV, GATE>;
-            case 4: return recurrent_kernel<D, 4, TQK, TV, GATE>;
-            case 2: return recurrent_kernel<D, 2, TQK, TV, GATE>;
-            case 1: return recurrent_kernel<D, 1, TQK, TV, GATE>;
+        switch (shape) {
+            case kDecode16: return recurrent_kernel<D, 32, 2, false, false, TQK, TV, GATE>;
+            case kDecode8: return recurrent_kernel<D, 32, 1, false, false, TQK, TV, GATE>;
+            case kMulti32: return recurrent_kernel<D, 32, 4, false, true, TQK, TV, GATE>;
+            case kMulti64: return recurrent_kernel<D, 16, 4, true, true, TQK, TV, GATE>;
             default: return nullptr;
         }
     } else {
-        switch (np) {
-            case 4: return recurrent_kernel<D, 4, TQK, TV, GATE>;
-            case 1: return recurrent_kernel<D, 1, TQK, TV, GATE>;
+        switch (shape) {
+            case kD64Large: return recurrent_kernel<D, 16, 4, false, false, TQK, TV, GATE>;
+            case kD64Small: return recurrent_kernel<D, 16, 1, false, false, TQK, TV, GATE>;
             default: return nullptr;
         }
     }
 }
 
 template <int D>
-KernelFn pick_kernel(int gate, int qk_dtype, int v_dtype, int np) {
+KernelFn pick_kernel(int gate, int qk_dtype, int v_dtype, Shape shape) {
     if (gate == KDA_GATE_RAW) {
         if (qk_dtype == KDA_BF16 && v_dtype == KDA_BF16) {
-            return pick_np<D, uint16_t, uint16_t, KDA_GATE_RAW>(np);
+            return pick_shape<D, uint16_t, uint16_t, KDA_GATE_RAW>(shape);
         }
         return nullptr;
     }
     if (gate == KDA_GATE_LOG) {
         if (qk_dtype == KDA_BF16 && v_dtype == KDA_BF16) {
-            return pick_np<D, uint16_t, uint16_t, KDA_GATE_LOG>(np);
+            return pick_shape<D, uint16_t, uint16_t, KDA_GATE_LOG>(shape);
         }
         if (qk_dtype == KDA_F32 && v_dtype == KDA_F32) {
-            return pick_np<D, float, float, KDA_GATE_LOG>(np);
+            return pick_shape<D, float, float, KDA_GATE_LOG>(shape);
         }
         return nullptr;
     }
     if (gate == KDA_GATE_DECAY) {
         if (qk_dtype == KDA_F32 && v_dtype == KDA_BF16) {
-            return pick_np<D, float, uint16_t, KDA_GATE_DECAY>(np);
+            return pick_shape<D, float, uint16_t, KDA_GATE_DECAY>(shape);
         }
         if (qk_dtype == KDA_F32 && v_dtype == KDA_F32) {
-            return pick_np<D, float, float, KDA_GATE_DECAY>(np);
+            return pick_shape<D, float, float, KDA_GATE_DECAY>(shape);
         }
         return nullptr;
     }
@@ -382,41 +566,58 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
     if (kargs.head_count == 0 || kargs.head_begin + kargs.head_count > kargs.num_heads) {
         kargs.head_count = kargs.num_heads - kargs.head_begin;
     }
-    // V-split at D=128, by tokens per sequence (measured on MI355X): one token
-    // (decode) -> 16-row tiles, eight workgroups per (sequence, head): 6.3 TB/s
-    // at B=256, H=32 against 6.05 with 32-row tiles; two tokens -> 32-row
-    // tiles; more (verify, recurrent prefill) -> 64-row tiles, which spread
-    // the per-token work (token loads, norms, reductions) over more rows
-    // (4 tokens x 1024 sequences, H=16: 456 us against 498 with 32-row tiles).
-    // Small batches use 8-row tiles so the launch still fills the GPU.
+    // Tile shape at D=128, by tokens per sequence (measured on MI355X,
+    // interleaved A/B on one box): one token (decode) -> 32-lane rows, 2 rows
+    // per lane: 16-row tiles, eight workgroups per (sequence, head), which
+    // stream the state fastest (B=256, H=32: 173 us, against 182 with
+    // 32-row tiles); two tokens -> 32-lane rows, 4 rows per lane (32-row
+    // tiles: 361 us at 512 x 2 tokens, H=32, against 367 with 16-lane
+    // rows); more (verify, recurrent prefill) -> 16-lane rows, whose
+    // reductions take four DPP steps instead of five plus a swizzle, 4
+    // consecutive rows per lane (64-row tiles), so each token's loads and
+    // exponentials serve more rows (1024 x 4 tokens, H=16: 406 us against
+    // 432 with 32-lane rows; 256 x 8 tokens, H=32: 283 against 351).
+    // Fewer than 128 (sequence, head) pairs use 8-row tiles so the launch
+    // still fills the GPU.
     const int64_t pairs = static_cast<int64_t>(a.num_seqs) * kargs.head_count;
+    Shape shape;
+    int rows_per_wg;
     int np;
     if (D == 128) {
         const int64_t tokens = a.num_tokens;
         if (pairs < 128) {
-            np = 1;
+            shape = kDecode8;
         } else if (tokens <= a.num_seqs) {
-            np = 2;
+            shape = kDecode16;
         } else if (tokens <= 2 * static_cast<int64_t>(a.num_seqs)) {
-            np = 4;
+            shape = kMulti32;
         } else {
-            np = 8;
+            shape = kMulti64;
         }
+        rows_per_wg = shape == kDecode8 ? 8 : shape == kDecode16 ? 16 : shape == kMulti32 ? 32 : 64;
+        np = shape == kDecode8 ? 1 : shape == kDecode16 ? 2 : 4;
     } else {
-        np = pairs >= 2048 ? 4 : 1;
+        shape = pairs >= 2048 ? kD64Large : kD64Small;
+        rows_per_wg = shape == kD64Large ? 64 : 16;
+        np = shape == kD64Large ? 4 : 1;
     }
-    KernelFn fn = (D == 128) ? pick_kernel<128>(a.gate_mode, a.qk_dtype, a.v_dtype, np)
-                             : pick_kernel<64>(a.gate_mode, a.qk_dtype, a.v_dtype, np);
+    KernelFn fn = (D == 128) ? pick_kernel<128>(a.gate_mode, a.qk_dtype, a.v_dtype, shape)
+                             : pick_kernel<64>(a.gate_mode, a.qk_dtype, a.v_dtype, shape);
     if (fn == nullptr) {
         return KDA_ERR_UNSUPPORTED;
     }
-    const int rows_per_wg = np * 4 * (64 / (D / 4));
+    // v rows are read and output rows written np values at a time when the
+    // tensors allow it (a lane's rows are consecutive, np-aligned).
+    const size_t vbytes = static_cast<size_t>(np) * (a.v_dtype == KDA_F32 ? 4 : 2);
+    const size_t vwant = vbytes > 16 ? 16 : vbytes;
+    int vec_io = ((reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out)) &
+                  (vwant - 1)) == 0;
     const int vts = D / rows_per_wg;
     const int64_t blocks = vts == 1 ? pairs : (pairs + 7) / 8 * 8 * vts;
     if (blocks > 0x7fffffff) {
         return KDA_ERR_INVALID_ARGUMENT;
     }
-    void *params[] = {&kargs};
+    void *params[] = {&kargs, &vec_io};
     const hipError_t err =
         hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3(static_cast<unsigned>(blocks)),
                         dim3(kThreads), params, 0, static_cast<hipStream_t>(stream));

@@ -351,6 +351,81 @@ def test_c_abi_launch_direct(gpu_ops):
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "state")
 
 
+def _shifted(x, shift):
+    """``x`` on the device at a storage offset of ``shift`` elements (so a
+    nonzero shift leaves it misaligned for vector access), plus the flat
+    buffer that owns it."""
+    flat = torch.zeros(x.numel() + shift, dtype=x.dtype, device=DEV)
+    view = flat[shift:].view(x.shape)
+    view.copy_(x.to(DEV))
+    return view, flat
+
+
+# (gate mode, q/k dtype, v dtype): the prepared forms the launcher accepts.
+_FORMS = {
+    "log-bf16": (1, torch.bfloat16, torch.bfloat16),
+    "log-f32": (1, torch.float32, torch.float32),
+    "decay-f32-bf16": (2, torch.float32, torch.bfloat16),
+    "decay-f32": (2, torch.float32, torch.float32),
+}
+_KDA_DTYPE = {torch.bfloat16: 0, torch.float32: 1}
+
+
+@pytest.mark.parametrize("shift", [0, 1], ids=["aligned", "misaligned"])
+@pytest.mark.parametrize("form", sorted(_FORMS))
+@pytest.mark.parametrize("lengths", [(1,) * 128, (2,) * 8, (4,) * 8, (1, 7, 3, 5, 2, 6, 4, 8)],
+                         ids=["decode", "2tok", "4tok", "ragged"])
+def test_tile_shapes_and_io_forms(gpu_ops, lengths, form, shift):
+    """Every tile shape the launcher picks for D=128 with at least 128
+    (sequence, head) pairs (one token: 32-lane rows, 16-row tiles; two
+    tokens per sequence: 32-lane rows, 32-row tiles; more: 16-lane rows,
+    64-row tiles whose v and o rows move as vectors), in every prepared input
+    form, with v and out aligned or shifted by one element (the per-element
+    path), through the C ABI, against the oracle."""
+    from sgl_glm53_ascend_ops._load import abi_library_path
+
+    mode, qk_dt, v_dt = _FORMS[form]
+    heads = 16 if len(lengths) == 8 else 1
+    case = C.prepared_case(heads, lengths, D=128, dtype=torch.float32,
+                           seed=400 + sum(lengths) + mode)
+    q, k = case.q.to(qk_dt), case.k.to(qk_dt)
+    v = case.v.to(v_dt)
+    gate = case.g if mode == 1 else torch.exp(case.g)
+    dq, dk = q.to(DEV), k.to(DEV)
+    dg, db = gate.to(DEV), case.beta.to(DEV)
+    dv, _v_owner = _shifted(v, shift)
+    out, _o_owner = _shifted(torch.zeros(v.shape, dtype=v_dt), shift)
+    pool = C.to_dev(case.pool, DEV)
+    idx = case.indices.to(DEV)
+    cu = case.cu_seqlens.to(DEV)
+    T, H, D = q.shape[1:]
+    lib = ctypes.CDLL(str(abi_library_path()))
+    lib.kda_recurrent_launch.argtypes = [ctypes.POINTER(_Args), ctypes.c_void_p]
+    lib.kda_recurrent_launch.restype = ctypes.c_int
+    a = _Args(q=dq.data_ptr(), k=dk.data_ptr(), v=dv.data_ptr(), gate=dg.data_ptr(),
+              beta=db.data_ptr(), state=pool.data_ptr(), state_stride_slot=pool.stride(0),
+              state_stride_head=pool.stride(1), num_slots=pool.shape[0],
+              state_indices=idx.data_ptr(), cu_seqlens=cu.data_ptr(), out=out.data_ptr(),
+              scale=case.scale, num_seqs=len(lengths), num_tokens=T, num_heads=H, head_begin=0,
+              head_count=H, head_dim=D, qk_dtype=_KDA_DTYPE[qk_dt], v_dtype=_KDA_DTYPE[v_dt],
+              gate_mode=mode, qk_l2norm=0)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.kda_recurrent_launch(ctypes.byref(a), ctypes.c_void_p(stream)) == 0
+    torch.cuda.synchronize()
+    ref_pool = C.clone_pool(case.pool)
+    ref = R.kda_recurrent(q.float() * case.scale, k, v, case.g, case.beta, state_pool=ref_pool,
+                          state_indices=case.indices, cu_seqlens=case.cu_seqlens,
+                          out_dtype=torch.float32)
+    if v_dt == torch.bfloat16:
+        C.assert_out(out.cpu(), ref, C.OUT_TOL, f"{form} output")
+    else:
+        assert C.max_rel_err(out.cpu(), ref) < 1e-5, f"{form} output"
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, f"{form} state")
+    if shift:
+        # the element before the shifted output is never written
+        assert _o_owner[0].item() == 0
+
+
 def test_config5_decode_full_size(gpu_ops):
     """BASELINE config 5's decode half at full size: 1024 sequences x 4 tokens,
     H=16, harsh decay, 2048-slot pool. Sequences are independent, so a seeded
