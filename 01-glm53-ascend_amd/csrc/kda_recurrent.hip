@@ -28,7 +28,8 @@
 // token with few rows per lane, so the launch has many small workgroups to
 // stream the state; three or more (verify, prefill) use 16-lane rows, whose
 // reductions take four DPP steps instead of five plus an LDS swizzle, with
-// four rows per lane to share each token's loads, exponentials and norms.
+// up to eight rows per lane to share each token's loads, exponentials and
+// norms.
 
 #include <hip/hip_runtime.h>
 
@@ -459,7 +460,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
 using KernelFn = void (*)(const KdaRecurrentArgs, int);
 
 // Tile shapes: (lanes per row L, rows per lane NP).
-enum Shape { kDecode16, kDecode8, kMulti32, kMulti64, kD64Small, kD64Large };
+enum Shape { kDecode16, kDecode8, kMulti32, kMulti64, kMulti128, kD64Small, kD64Large };
 
 template <int D, typename TQK, typename TV, int GATE>
 KernelFn pick_shape(Shape shape) {
@@ -469,6 +470,7 @@ KernelFn pick_shape(Shape shape) {
             case kDecode8: return recurrent_kernel<D, 32, 1, false, false, TQK, TV, GATE>;
             case kMulti32: return recurrent_kernel<D, 32, 4, false, true, TQK, TV, GATE>;
             case kMulti64: return recurrent_kernel<D, 16, 4, true, true, TQK, TV, GATE>;
+            case kMulti128: return recurrent_kernel<D, 16, 8, true, true, TQK, TV, GATE>;
             default: return nullptr;
         }
     } else {
@@ -573,12 +575,14 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
     // 32-row tiles); two tokens -> 32-lane rows, 4 rows per lane (32-row
     // tiles: 361 us at 512 x 2 tokens, H=32, against 367 with 16-lane
     // rows); more (verify, recurrent prefill) -> 16-lane rows, whose
-    // reductions take four DPP steps instead of five plus a swizzle, 4
-    // consecutive rows per lane (64-row tiles), so each token's loads and
-    // exponentials serve more rows (1024 x 4 tokens, H=16: 406 us against
-    // 432 with 32-lane rows; 256 x 8 tokens, H=32: 283 against 351).
-    // Fewer than 128 (sequence, head) pairs use 8-row tiles so the launch
-    // still fills the GPU.
+    // reductions take four DPP steps instead of five plus a swizzle, with 8
+    // consecutive rows per lane (the whole state of a (sequence, head) in one
+    // workgroup) so each token's loads and exponentials serve more rows:
+    // 1024 x 4 tokens, H=16: 382 us, against 406 with 4 rows per lane, 464
+    // with 2 and 432 with 32-lane rows; 256 x 8 tokens, H=32: 265 against
+    // 284 and 351. The 8-row-per-lane shape runs three workgroups per CU, so
+    // below 1024 pairs the 4-row one (two workgroups per pair) fills the GPU
+    // instead. Fewer than 128 pairs use 8-row tiles, 32 lanes per row.
     const int64_t pairs = static_cast<int64_t>(a.num_seqs) * kargs.head_count;
     Shape shape;
     int rows_per_wg;
@@ -591,11 +595,17 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
             shape = kDecode16;
         } else if (tokens <= 2 * static_cast<int64_t>(a.num_seqs)) {
             shape = kMulti32;
-        } else {
+        } else if (pairs < 1024) {
             shape = kMulti64;
+        } else {
+            shape = kMulti128;
         }
-        rows_per_wg = shape == kDecode8 ? 8 : shape == kDecode16 ? 16 : shape == kMulti32 ? 32 : 64;
-        np = shape == kDecode8 ? 1 : shape == kDecode16 ? 2 : 4;
+        rows_per_wg = shape == kDecode8    ? 8
+                      : shape == kDecode16 ? 16
+                      : shape == kMulti32  ? 32
+                      : shape == kMulti64  ? 64
+                                           : 128;
+        np = shape == kDecode8 ? 1 : shape == kDecode16 ? 2 : shape == kMulti128 ? 8 : 4;
     } else {
         shape = pairs >= 2048 ? kD64Large : kD64Small;
         rows_per_wg = shape == kD64Large ? 64 : 16;

@@ -373,19 +373,20 @@ _KDA_DTYPE = {torch.bfloat16: 0, torch.float32: 1}
 
 @pytest.mark.parametrize("shift", [0, 1], ids=["aligned", "misaligned"])
 @pytest.mark.parametrize("form", sorted(_FORMS))
-@pytest.mark.parametrize("lengths", [(1,) * 128, (2,) * 8, (4,) * 8, (1, 7, 3, 5, 2, 6, 4, 8)],
-                         ids=["decode", "2tok", "4tok", "ragged"])
-def test_tile_shapes_and_io_forms(gpu_ops, lengths, form, shift):
+@pytest.mark.parametrize("lengths,heads", [((1,) * 128, 1), ((2,) * 8, 16), ((4,) * 8, 16),
+                                           ((1, 7, 3, 5, 2, 6, 4, 8), 16), ((3,) * 64, 16)],
+                         ids=["decode", "2tok", "4tok", "ragged", "3tok-1024pairs"])
+def test_tile_shapes_and_io_forms(gpu_ops, lengths, heads, form, shift):
     """Every tile shape the launcher picks for D=128 with at least 128
     (sequence, head) pairs (one token: 32-lane rows, 16-row tiles; two
     tokens per sequence: 32-lane rows, 32-row tiles; more: 16-lane rows,
-    64-row tiles whose v and o rows move as vectors), in every prepared input
-    form, with v and out aligned or shifted by one element (the per-element
-    path), through the C ABI, against the oracle."""
+    64-row tiles, or 128-row tiles from 1024 pairs, whose v and o rows move
+    as vectors), in every prepared input form, with v and out aligned or
+    shifted by one element (the per-element path), through the C ABI,
+    against the oracle."""
     from sgl_glm53_ascend_ops._load import abi_library_path
 
     mode, qk_dt, v_dt = _FORMS[form]
-    heads = 16 if len(lengths) == 8 else 1
     case = C.prepared_case(heads, lengths, D=128, dtype=torch.float32,
                            seed=400 + sum(lengths) + mode)
     q, k = case.q.to(qk_dt), case.k.to(qk_dt)
