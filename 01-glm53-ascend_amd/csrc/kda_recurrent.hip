@@ -69,98 +69,106 @@ template <> struct Raw4<float> {
     __device__ __forceinline__ float4 get() const { return r; }
 };
 
-// NP values of one token row (v in, o out), RS elements apart. Consecutive
-// ones (RS = 1) whose segment is aligned to its size (`vec`, up to 16
-// bytes) move in as few vector accesses as that allows; otherwise element
-// by element.
-template <typename T, int NP> struct RowVec {
-    float x[NP];
-    template <int RS>
-    __device__ __forceinline__ void load(const T *p, bool vec) {
-        if constexpr (RS == 1 && sizeof(T) == 2 && NP >= 2) {
-            if (vec) {
-                uint32_t w[NP / 2];
-                if constexpr (NP == 2) {
-                    w[0] = *reinterpret_cast<const uint32_t *>(p);
-                } else if constexpr (NP == 4) {
-                    const uint2 u = *reinterpret_cast<const uint2 *>(p);
-                    w[0] = u.x;
-                    w[1] = u.y;
-                } else {
+// NP values of one v row, RS elements apart, as loaded (widened at use, so
+// the load is not waited for until the value is needed). Consecutive values
+// (RS = 1; the host guarantees the segment is aligned to its size) arrive in
+// 16-byte or smaller vectors: bf16 pairs packed in words, fp32 as is. Spread
+// ones arrive one element per load.
+template <typename T, int NP, int RS> struct RowIn;
+template <int NP, int RS> struct RowIn<uint16_t, NP, RS> {
+    static constexpr int W = RS == 1 ? NP / 2 : NP;
+    static_assert(RS != 1 || NP % 2 == 0, "bf16 pairs");
+    uint32_t w[W];
+    __device__ __forceinline__ void load(const uint16_t *p) {
+        if constexpr (RS != 1) {
 #pragma unroll
-                    for (int i = 0; i < NP / 8; ++i) {
-                        const uint4 u = reinterpret_cast<const uint4 *>(p)[i];
-                        w[4 * i + 0] = u.x;
-                        w[4 * i + 1] = u.y;
-                        w[4 * i + 2] = u.z;
-                        w[4 * i + 3] = u.w;
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < NP / 2; ++i) {
-                    x[2 * i] = __uint_as_float(w[i] << 16);
-                    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-                }
-                return;
+            for (int i = 0; i < NP; ++i) {
+                w[i] = p[RS * i];
             }
-        } else if constexpr (RS == 1 && sizeof(T) == 4 && NP >= 4) {
-            if (vec) {
+        } else if constexpr (NP == 2) {
+            w[0] = *reinterpret_cast<const uint32_t *>(p);
+        } else if constexpr (NP == 4) {
+            const uint2 u = *reinterpret_cast<const uint2 *>(p);
+            w[0] = u.x;
+            w[1] = u.y;
+        } else {
 #pragma unroll
-                for (int i = 0; i < NP / 4; ++i) {
-                    const float4 u = reinterpret_cast<const float4 *>(p)[i];
-                    x[4 * i + 0] = u.x;
-                    x[4 * i + 1] = u.y;
-                    x[4 * i + 2] = u.z;
-                    x[4 * i + 3] = u.w;
-                }
-                return;
+            for (int i = 0; i < NP / 8; ++i) {
+                const uint4 u = reinterpret_cast<const uint4 *>(p)[i];
+                w[4 * i + 0] = u.x;
+                w[4 * i + 1] = u.y;
+                w[4 * i + 2] = u.z;
+                w[4 * i + 3] = u.w;
             }
-        }
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            x[i] = load1(p + RS * i);
         }
     }
-    // Written by the row group's lanes kc: consecutive values by lane 0 as
-    // one vector when allowed, else value i by lane i (kc < NP).
-    template <int RS>
-    __device__ __forceinline__ void store_by(T *p, bool vec, int kc) const {
-        if constexpr (RS == 1 && sizeof(T) == 2 && NP >= 2) {
-            if (vec) {
-                if (kc != 0) {
-                    return;
-                }
-                uint32_t w[NP / 2];
+    __device__ __forceinline__ float get(int i) const {
+        if constexpr (RS != 1) {
+            return __uint_as_float(w[i] << 16);
+        } else {
+            return __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+        }
+    }
+};
+template <int NP, int RS> struct RowIn<float, NP, RS> {
+    static_assert(RS != 1 || NP % 4 == 0, "whole float4 vectors");
+    float x[NP];
+    __device__ __forceinline__ void load(const float *p) {
+        if constexpr (RS != 1) {
 #pragma unroll
-                for (int i = 0; i < NP / 2; ++i) {
-                    w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-                }
-                if constexpr (NP == 2) {
-                    *reinterpret_cast<uint32_t *>(p) = w[0];
-                } else if constexpr (NP == 4) {
-                    *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < NP / 8; ++i) {
-                        reinterpret_cast<uint4 *>(p)[i] =
-                            make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
-                    }
-                }
-                return;
+            for (int i = 0; i < NP; ++i) {
+                x[i] = p[RS * i];
             }
-        } else if constexpr (RS == 1 && sizeof(T) == 4 && NP >= 4) {
-            if (vec) {
-                if (kc != 0) {
-                    return;
-                }
+        } else {
 #pragma unroll
-                for (int i = 0; i < NP / 4; ++i) {
-                    reinterpret_cast<float4 *>(p)[i] =
-                        make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
-                }
-                return;
+            for (int i = 0; i < NP / 4; ++i) {
+                const float4 u = reinterpret_cast<const float4 *>(p)[i];
+                x[4 * i + 0] = u.x;
+                x[4 * i + 1] = u.y;
+                x[4 * i + 2] = u.z;
+                x[4 * i + 3] = u.w;
             }
         }
+    }
+    __device__ __forceinline__ float get(int i) const { return x[i]; }
+};
+
+// NP output values of one row, RS elements apart, written by the row
+// group's lanes kc: consecutive ones by lane 0 as one vector, spread ones
+// value i by lane i.
+template <typename T, int NP, int RS>
+__device__ __forceinline__ void store_row(T *p, const float (&x)[NP], int kc) {
+    if constexpr (RS == 1) {
+        if (kc != 0) {
+            return;
+        }
+        if constexpr (sizeof(T) == 2) {
+            static_assert(NP % 2 == 0, "bf16 pairs");
+            uint32_t w[NP / 2];
+#pragma unroll
+            for (int i = 0; i < NP / 2; ++i) {
+                w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+            }
+            if constexpr (NP == 2) {
+                *reinterpret_cast<uint32_t *>(p) = w[0];
+            } else if constexpr (NP == 4) {
+                *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NP / 8; ++i) {
+                    reinterpret_cast<uint4 *>(p)[i] =
+                        make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+                }
+            }
+        } else {
+            static_assert(NP % 4 == 0, "whole float4 vectors");
+#pragma unroll
+            for (int i = 0; i < NP / 4; ++i) {
+                reinterpret_cast<float4 *>(p)[i] =
+                    make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+            }
+        }
+    } else {
         float mine = 0.f;
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -170,10 +178,10 @@ template <typename T, int NP> struct RowVec {
             store1(p + RS * kc, mine);
         }
     }
-};
+}
 
-template <int D, int L, int NP, bool CONTIG, bool FEXP, typename TQK, typename TV, int GATE>
-__global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentArgs a, int vec_io) {
+template <int D, int L, int NP, bool CONTIG, int TPS, typename TQK, typename TV, int GATE>
+__global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentArgs a) {
     constexpr int E = D / L;           // K elements per lane
     constexpr int EV = E / 4;          // 16-byte vectors per lane and row
     constexpr int RPW = 64 / L;        // row groups per wave
@@ -183,10 +191,11 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     // per row group) or RPP apart (each wave-wide state load then covers
     // RPW adjacent rows, one contiguous span).
     constexpr int RS = CONTIG ? 1 : RPP;
-    // The decay's exponential: one v_exp_f32 (FEXP) where the token loop's
-    // instruction count matters (several tokens per sequence), the correctly
-    // rounded expf where the launch is bound by the state traffic (decode).
-    auto dexp = [](float x) { return FEXP ? fexp(x) : expf(x); };
+    // TPS: the tokens per sequence a shape is tuned for -- 1 (decode), 2, or
+    // 3 and more. With several, the token loop's instruction count matters
+    // and the exponentials are one v_exp_f32 each; decode, bound by the
+    // state traffic, keeps the correctly rounded expf.
+    auto dexp = [](float x) { return TPS > 1 ? fexp(x) : expf(x); };
     constexpr int VT = D / RB;         // workgroups per (sequence, head)
     static_assert(E % 4 == 0 && D % RB == 0, "whole vectors and whole row tiles");
 
@@ -210,7 +219,6 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     const int rgw = wave * RPW + lane / L;  // row group in the workgroup
     const int row0 = vt * RB + (CONTIG ? rgw * NP : rgw);  // rows row0 + RS*p, p < NP
     const int T = a.num_tokens;
-    const bool vec = vec_io != 0;
 
     int bos = a.cu_seqlens[n];
     int eos = a.cu_seqlens[n + 1];
@@ -296,15 +304,14 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     using TG = typename std::conditional<GATE == KDA_GATE_RAW, uint16_t, float>::type;
     const TG *gp = static_cast<const TG *>(a.gate);
 
-    // One token's inputs, as loaded (widened and transformed at use). The
-    // next token's are loaded while the current one computes: a multi-token
-    // sequence (verify, prefill) would otherwise wait a full load latency per
-    // token. (Unrolling by two to alternate the buffers without copies costs
-    // more registers than the copies cost instructions.)
+    // One token's inputs, as loaded; widened and transformed before its
+    // step. The next token's are loaded while the current one computes: a
+    // multi-token sequence (verify, prefill) would otherwise wait a full load
+    // latency per token.
     struct TokenIn {
         Raw4<TQK> q[EV], k[EV];
         Raw4<TG> g[EV];
-        RowVec<TV, NP> v;
+        RowIn<TV, NP, RS> v;
         float b;
     };
     auto fetch = [&](int t, TokenIn &in) {
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
             in.k[j].load(kp + base + koff(j));
             in.g[j].load(gp + base + koff(j));
         }
-        in.v.template load<RS>(vp + base + row0, vec);
+        in.v.load(vp + base + row0);
         const int64_t bi = static_cast<int64_t>(t) * H + head;
         if constexpr (GATE == KDA_GATE_RAW) {
             in.b = bf16_to_f32(static_cast<const uint16_t *>(a.beta)[bi]);
@@ -323,31 +330,39 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
             in.b = static_cast<const float *>(a.beta)[bi];
         }
     };
-    auto step = [&](const TokenIn &in, int t) {
-        float4 qv[EV], kv[EV], dec[EV];
+    // A token ready for the update: scaled q, normalized k, decay, beta, v.
+    struct Token {
+        float4 q[EV], k[EV], dec[EV];
         float beta;
+        float v[NP];
+    };
+    auto widen = [&](const TokenIn &in, Token &w) {
 #pragma unroll
         for (int j = 0; j < EV; ++j) {
-            qv[j] = in.q[j].get();
-            kv[j] = in.k[j].get();
+            w.q[j] = in.q[j].get();
+            w.k[j] = in.k[j].get();
             const float4 gv = in.g[j].get();
             if constexpr (GATE == KDA_GATE_RAW) {
                 // g = lower_bound / (1 + exp(-(exp(A_log) * (a + dt_bias)))), decay = exp(g)
                 const float lb = a.lower_bound;
-                dec[j].x = dexp(lb / (1.0f + dexp(-(expA * (gv.x + dtb[j].x)))));
-                dec[j].y = dexp(lb / (1.0f + dexp(-(expA * (gv.y + dtb[j].y)))));
-                dec[j].z = dexp(lb / (1.0f + dexp(-(expA * (gv.z + dtb[j].z)))));
-                dec[j].w = dexp(lb / (1.0f + dexp(-(expA * (gv.w + dtb[j].w)))));
+                w.dec[j].x = dexp(lb / (1.0f + dexp(-(expA * (gv.x + dtb[j].x)))));
+                w.dec[j].y = dexp(lb / (1.0f + dexp(-(expA * (gv.y + dtb[j].y)))));
+                w.dec[j].z = dexp(lb / (1.0f + dexp(-(expA * (gv.z + dtb[j].z)))));
+                w.dec[j].w = dexp(lb / (1.0f + dexp(-(expA * (gv.w + dtb[j].w)))));
             } else if constexpr (GATE == KDA_GATE_LOG) {
-                dec[j] = make_float4(dexp(gv.x), dexp(gv.y), dexp(gv.z), dexp(gv.w));
+                w.dec[j] = make_float4(dexp(gv.x), dexp(gv.y), dexp(gv.z), dexp(gv.w));
             } else {
-                dec[j] = gv;
+                w.dec[j] = gv;
             }
         }
         if constexpr (GATE == KDA_GATE_RAW) {
-            beta = 1.0f / (1.0f + dexp(-in.b));
+            w.beta = 1.0f / (1.0f + dexp(-in.b));
         } else {
-            beta = in.b;
+            w.beta = in.b;
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            w.v[p] = in.v.get(p);
         }
         float qsc = a.scale;
         if (norm) {
@@ -355,8 +370,8 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
             float qs = 0.f, ks = 0.f;
 #pragma unroll
             for (int j = 0; j < EV; ++j) {
-                qs += dot4(qv[j], qv[j]);
-                ks += dot4(kv[j], kv[j]);
+                qs += dot4(w.q[j], w.q[j]);
+                ks += dot4(w.k[j], w.k[j]);
             }
             qs = group_sum<L>(qs);
             ks = group_sum<L>(ks);
@@ -364,46 +379,55 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
             qsc = (1.0f / sqrtf(qs + 1e-6f)) * a.scale;
 #pragma unroll
             for (int j = 0; j < EV; ++j) {
-                kv[j] = make_float4(kv[j].x * kr, kv[j].y * kr, kv[j].z * kr, kv[j].w * kr);
+                w.k[j] = make_float4(w.k[j].x * kr, w.k[j].y * kr, w.k[j].z * kr, w.k[j].w * kr);
             }
         }
 #pragma unroll
         for (int j = 0; j < EV; ++j) {
-            qv[j] = make_float4(qv[j].x * qsc, qv[j].y * qsc, qv[j].z * qsc, qv[j].w * qsc);
+            w.q[j] = make_float4(w.q[j].x * qsc, w.q[j].y * qsc, w.q[j].z * qsc, w.q[j].w * qsc);
         }
-
+    };
+    // sum over the lane's E elements of s * x, one multiply-add chain
+    auto dot_lane = [](const float4 (&sv)[EV], const float4 (&xv)[EV]) {
+        float acc = dot4(sv[0], xv[0]);
+#pragma unroll
+        for (int j = 1; j < EV; ++j) {
+            acc = fmaf(sv[j].x, xv[j].x, acc);
+            acc = fmaf(sv[j].y, xv[j].y, acc);
+            acc = fmaf(sv[j].z, xv[j].z, acc);
+            acc = fmaf(sv[j].w, xv[j].w, acc);
+        }
+        return acc;
+    };
+    auto step = [&](const Token &w, int t) {
         float pred[NP];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            float acc = 0.f;
 #pragma unroll
             for (int j = 0; j < EV; ++j) {
-                S[p][j].x *= dec[j].x;
-                S[p][j].y *= dec[j].y;
-                S[p][j].z *= dec[j].z;
-                S[p][j].w *= dec[j].w;
-                acc += dot4(S[p][j], kv[j]);
+                S[p][j].x *= w.dec[j].x;
+                S[p][j].y *= w.dec[j].y;
+                S[p][j].z *= w.dec[j].z;
+                S[p][j].w *= w.dec[j].w;
             }
-            pred[p] = acc;
+            pred[p] = dot_lane(S[p], w.k);
         }
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             pred[p] = group_sum<L>(pred[p]);
         }
-        RowVec<TV, NP> o;
+        float o[NP];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            const float d = (in.v.x[p] - pred[p]) * beta;
-            float acc = 0.f;
+            const float d = (w.v[p] - pred[p]) * w.beta;
 #pragma unroll
             for (int j = 0; j < EV; ++j) {
-                S[p][j].x += kv[j].x * d;
-                S[p][j].y += kv[j].y * d;
-                S[p][j].z += kv[j].z * d;
-                S[p][j].w += kv[j].w * d;
-                acc += dot4(S[p][j], qv[j]);
+                S[p][j].x += w.k[j].x * d;
+                S[p][j].y += w.k[j].y * d;
+                S[p][j].z += w.k[j].z * d;
+                S[p][j].w += w.k[j].w * d;
             }
-            o.x[p] = acc;
+            o[p] = dot_lane(S[p], w.q);
         }
         const int step_i = t - bos;
         if (save_mid && step_i < a.mid_steps) {
@@ -415,34 +439,57 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
         }
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            o.x[p] = group_sum<L>(o.x[p]);
+            o[p] = group_sum<L>(o[p]);
         }
         // every lane of the row group holds the sums
-        o.template store_by<RS>(op + (static_cast<int64_t>(t) * H + head) * D + row0, vec, kc);
+        store_row<TV, NP, RS>(op + (static_cast<int64_t>(t) * H + head) * D + row0, o, kc);
     };
-    TokenIn cur, nxt;
-    if (bos < eos) {
-        fetch(bos, cur);
-    }
-    for (int t = bos; t < eos; ++t) {
-        if (t + 1 < eos) {
-            fetch(t + 1, nxt);
+    if constexpr (TPS > 2) {
+        // One buffer: the next token's loads are issued into it right after
+        // the current token is widened, unconditionally (the last token
+        // reloads itself), so the buffer is always reloaded, never kept --
+        // keeping it would cost register copies and a wait for every
+        // outstanding store on the way back to the loop's top.
+        if (bos < eos) {
+            TokenIn in;
+            fetch(bos, in);
+            for (int t = bos; t < eos; ++t) {
+                Token w;
+                widen(in, w);
+                fetch(t + 1 < eos ? t + 1 : t, in);
+                step(w, t);
+            }
         }
-        step(cur, t);
-        cur = nxt;
+    } else {
+        // One or two tokens per sequence: a second buffer, loaded only when
+        // a next token exists (an unconditional reload would be a third of
+        // the token loads at two tokens, all of them at one).
+        TokenIn cur, nxt;
+        if (bos < eos) {
+            fetch(bos, cur);
+        }
+        for (int t = bos; t < eos; ++t) {
+            if (t + 1 < eos) {
+                fetch(t + 1, nxt);
+            }
+            Token w;
+            widen(cur, w);
+            step(w, t);
+            cur = nxt;
+        }
     }
 
     // Tokens no sequence covers are zero (the reference allocates
     // zeros_like(v), kda_varlen_recurrent.cpp:142): the first request zeroes
     // [0, cu[0]) and the last one [cu[N], T).
     auto zero_rows = [&](int t0, int t1) {
-        RowVec<TV, NP> z;
+        float z[NP];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            z.x[p] = 0.f;
+            z[p] = 0.f;
         }
         for (int t = t0; t < t1; ++t) {
-            z.template store_by<RS>(op + (static_cast<int64_t>(t) * H + head) * D + row0, vec, kc);
+            store_row<TV, NP, RS>(op + (static_cast<int64_t>(t) * H + head) * D + row0, z, kc);
         }
     };
     if (n == 0) {
@@ -457,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     }
 }
 
-using KernelFn = void (*)(const KdaRecurrentArgs, int);
+using KernelFn = void (*)(const KdaRecurrentArgs);
 
 // Tile shapes: (lanes per row L, rows per lane NP).
 enum Shape { kDecode16, kDecode8, kMulti32, kMulti64, kMulti128, kD64Small, kD64Large };
@@ -466,17 +513,17 @@ template <int D, typename TQK, typename TV, int GATE>
 KernelFn pick_shape(Shape shape) {
     if constexpr (D == 128) {
         switch (shape) {
-            case kDecode16: return recurrent_kernel<D, 32, 2, false, false, TQK, TV, GATE>;
-            case kDecode8: return recurrent_kernel<D, 32, 1, false, false, TQK, TV, GATE>;
-            case kMulti32: return recurrent_kernel<D, 32, 4, false, true, TQK, TV, GATE>;
-            case kMulti64: return recurrent_kernel<D, 16, 4, true, true, TQK, TV, GATE>;
-            case kMulti128: return recurrent_kernel<D, 16, 8, true, true, TQK, TV, GATE>;
+            case kDecode16: return recurrent_kernel<D, 32, 2, false, 1, TQK, TV, GATE>;
+            case kDecode8: return recurrent_kernel<D, 32, 1, false, 1, TQK, TV, GATE>;
+            case kMulti32: return recurrent_kernel<D, 32, 4, false, 2, TQK, TV, GATE>;
+            case kMulti64: return recurrent_kernel<D, 16, 4, true, 3, TQK, TV, GATE>;
+            case kMulti128: return recurrent_kernel<D, 16, 8, true, 3, TQK, TV, GATE>;
             default: return nullptr;
         }
     } else {
         switch (shape) {
-            case kD64Large: return recurrent_kernel<D, 16, 4, false, false, TQK, TV, GATE>;
-            case kD64Small: return recurrent_kernel<D, 16, 1, false, false, TQK, TV, GATE>;
+            case kD64Large: return recurrent_kernel<D, 16, 4, false, 1, TQK, TV, GATE>;
+            case kD64Small: return recurrent_kernel<D, 16, 1, false, 1, TQK, TV, GATE>;
             default: return nullptr;
         }
     }
@@ -586,7 +633,6 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
     const int64_t pairs = static_cast<int64_t>(a.num_seqs) * kargs.head_count;
     Shape shape;
     int rows_per_wg;
-    int np;
     if (D == 128) {
         const int64_t tokens = a.num_tokens;
         if (pairs < 128) {
@@ -600,34 +646,39 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
         } else {
             shape = kMulti128;
         }
+        // The 16-lane shapes move a lane's consecutive v and o values as one
+        // vector of up to 16 bytes; v or out not aligned for that take the
+        // 32-row shape, which moves them one element at a time.
+        if (shape == kMulti64 || shape == kMulti128) {
+            const size_t vbytes = static_cast<size_t>(shape == kMulti128 ? 8 : 4) *
+                                  (a.v_dtype == KDA_F32 ? 4 : 2);
+            const uintptr_t mis = (reinterpret_cast<uintptr_t>(a.v) |
+                                   reinterpret_cast<uintptr_t>(a.out)) &
+                                  ((vbytes > 16 ? 16 : vbytes) - 1);
+            if (mis != 0) {
+                shape = kMulti32;
+            }
+        }
         rows_per_wg = shape == kDecode8    ? 8
                       : shape == kDecode16 ? 16
                       : shape == kMulti32  ? 32
                       : shape == kMulti64  ? 64
                                            : 128;
-        np = shape == kDecode8 ? 1 : shape == kDecode16 ? 2 : shape == kMulti128 ? 8 : 4;
     } else {
         shape = pairs >= 2048 ? kD64Large : kD64Small;
         rows_per_wg = shape == kD64Large ? 64 : 16;
-        np = shape == kD64Large ? 4 : 1;
     }
     KernelFn fn = (D == 128) ? pick_kernel<128>(a.gate_mode, a.qk_dtype, a.v_dtype, shape)
                              : pick_kernel<64>(a.gate_mode, a.qk_dtype, a.v_dtype, shape);
     if (fn == nullptr) {
         return KDA_ERR_UNSUPPORTED;
     }
-    // v rows are read and output rows written np values at a time when the
-    // tensors allow it (a lane's rows are consecutive, np-aligned).
-    const size_t vbytes = static_cast<size_t>(np) * (a.v_dtype == KDA_F32 ? 4 : 2);
-    const size_t vwant = vbytes > 16 ? 16 : vbytes;
-    int vec_io = ((reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out)) &
-                  (vwant - 1)) == 0;
     const int vts = D / rows_per_wg;
     const int64_t blocks = vts == 1 ? pairs : (pairs + 7) / 8 * 8 * vts;
     if (blocks > 0x7fffffff) {
         return KDA_ERR_INVALID_ARGUMENT;
     }
-    void *params[] = {&kargs, &vec_io};
+    void *params[] = {&kargs};
     const hipError_t err =
         hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3(static_cast<unsigned>(blocks)),
                         dim3(kThreads), params, 0, static_cast<hipStream_t>(stream));
