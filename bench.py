@@ -57,6 +57,8 @@ FETCH_SCALE = 524288.0 / 262156.8
 WRITE_SCALE = 524288.0 / 524288.0
 DEC_FETCH_KIB, DEC_WRITE_KIB = 267451.4, 526336.2
 DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
+# Same for config 5's 4-token verify launch (1024 sequences, H=16).
+VF_TRAFFIC = (565882.7 * FETCH_SCALE + 1063961.9 * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
 PF_TRAFFIC = ((168219.6 + 261478.4) * FETCH_SCALE + (509952.0 + 108790.8) * WRITE_SCALE) * 1024
 # MFMA counters of the same two kernels (profiles/prefill_chunk_t8192_h32_mfma.md): matrix work
@@ -266,7 +268,8 @@ def run_more(steps=5, warmup=1):
     out["config5_decode"] = dict(seqs=n5, tokens_per_seq=steps5, heads=h5, pool_slots=slots5,
                                  kernel_us=us, tok_per_s=n5 * steps5 / (us * 1e-6),
                                  hbm_gbs=gbs, hbm_frac=gbs / HBM_PEAK_GBS,
-                                 algorithmic_bytes=nbytes)
+                                 algorithmic_bytes=nbytes, traffic=VF_TRAFFIC,
+                                 kernel="recurrent_kernel<128,16,8,consecutive rows,multi-token>")
     _log(f"config5_decode: {us:.1f} us, {gbs:.0f} GB/s")
     return out
 
@@ -455,7 +458,7 @@ def main():
         roofline=dict(
             bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
             frac=achieved / HBM_PEAK_GBS, traffic=DEC_TRAFFIC,
-            kernel="recurrent_kernel<128,2,bf16,bf16,LOG>",
+            kernel="recurrent_kernel<128,32,2,strided rows,decode,bf16,bf16,LOG>",
             algorithmic_bytes_per_launch=DEC_BYTES, kernel_us=dec["kernel_us"],
         ),
         prefill=prefill,
