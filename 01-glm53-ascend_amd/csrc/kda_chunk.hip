@@ -208,15 +208,16 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
 // ---------------------------------------------------------------------------
 // K1: per (chunk, head) intra-chunk work.
 //
-// About 71 KiB of LDS, so two workgroups share a CU and one's loads overlap
-// the other's math. Every global load of the chunk (k, g, beta, v and each
-// wave's q rows) is issued up front. k stays as its bf16 input plus a per-row
-// inverse norm; the decay is accumulated in log2 units, so each exponential is
-// one v_exp_f32. v and e^G k stay row-major and are read as MFMA operands with
-// gfx950's transposing LDS read ds_read_b64_tr_b16: within each group of 16
-// lanes, lane 16G + i receives as element m the (i % 4)-th 16-bit value of the
-// 8-byte word addressed by lane 16G + 4m + i / 4. The solve's X and the v tile
-// reuse the cumsum tile once it is dead.
+// 53 KiB of LDS (two workgroups per CU, which its registers also allow; at
+// three, forced, it ran no faster). The chunk's k, g, beta and each wave's q
+// rows are loaded up front, v after the cumsum and k tiles die. k stays as
+// its bf16 input plus a per-row inverse norm; the decay is accumulated in
+// log2 units, so each exponential is one v_exp_f32. v and e^G k stay
+// row-major and are read as MFMA operands with gfx950's transposing LDS read
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane 16G + i receives as
+// element m the (i % 4)-th 16-bit value of the 8-byte word addressed by lane
+// 16G + 4m + i / 4. X, LT and e^G k lie over the cumsum and k tiles once
+// those are dead, and v over X and LT in the last stage.
 // ---------------------------------------------------------------------------
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -254,24 +255,27 @@ __device__ __forceinline__ bf16x8 lds_tr_frag(const uint16_t *tile, int row0, in
 
 struct PrepShared {
     union {
-        float G[BT][kPadF];  // cumsum of the log2 decay (S1-S4)
         struct {
-            float X[BT][kPadX];     // (I + L)^-1, then T = X diag(beta) (S5-S6)
-            uint16_t V[BT][kPadT];  // v, bf16 bits, row-major (S5-S6)
+            float G[BT][kPadF];     // cumsum of the log2 decay (S1-S4)
+            uint16_t K[BT][kPadK];  // k, bf16 input bits (S1-S4)
+            float qss[2][BT];       // sum of q^2 over each channel half, per row (S1-S3)
+        } early;
+        struct {
+            float X[BT][kPadX];      // (I + L)^-1, then T = X diag(beta) (S5-S6)
+            // Strict upper triangle: L^T, LT[j][i] = beta_i Akk[i][j] (j < i).
+            // Lower triangle with the diagonal: Aqk[i][j] (j <= i).
+            float LT[BT][kPadX];
+            uint16_t KE[BT][kPadT];  // e^G k as bf16, row-major (S4-S6)
+        } mid;
+        struct {
+            uint16_t V[BT][kPadT];  // v, bf16 bits, row-major (S6, over the dead X and LT)
         } late;
-    } r0;
-    union {
-        uint16_t K[BT][kPadK];   // k, bf16 input bits (S1-S4)
-        uint16_t KE[BT][kPadT];  // e^G k as bf16, row-major (S4-S6)
-    } r1;
-    // Strict upper triangle: L^T, LT[j][i] = beta_i Akk[i][j] (j < i).
-    // Lower triangle with the diagonal: Aqk[i][j] (j <= i).
-    float LT[BT][kPadX];
+    } u;
     float beta[BT];
     float rnk[BT];        // k row scale (1 / norm, or 1)
     float carry[DK];
 };
-static_assert(sizeof(PrepShared) <= 80 * 1024, "two prepare workgroups per CU");
+static_assert(sizeof(PrepShared) <= 54 * 1024, "the prepare kernel's LDS budget");
 
 template <int GATE>
 __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkArgs a, char *ws,
@@ -322,24 +326,20 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     //        wave 2: (2,0) (1,0)   wave 3: (2,1) (1,1)
     const int sh = wave & 1;
     const int IA = wave < 2 ? 3 : 2;
-    // q rows of both blocks, loaded now so the loads overlap S1/S2: lane (r, gq)
-    // holds q[16I + r][32s + kperm(gq, e)] as 2 x (4 bf16) per slice; entries
-    // 0, 1 are this wave's slices, 2, 3 the other half's (read for the norm).
-    uint2 qraw[2][4][2];
+    // q rows of both blocks in this wave's channel half, loaded now so the
+    // loads overlap S1/S2: lane (r, gq) holds q[16I + r][32s + kperm(gq, e)]
+    // as 2 x (4 bf16) for slices s = 2 sh + q2.
+    uint2 qraw[2][2][2];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
         const int t = 16 * (ii == 0 ? IA : 3 - IA) + r;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const int s = q4 < 2 ? 2 * sh + q4 : 2 * (1 - sh) + (q4 - 2);
-            qraw[ii][q4][0] = make_uint2(0u, 0u);
-            qraw[ii][q4][1] = make_uint2(0u, 0u);
-            if (q4 < 2 || norm) {  // uniform
-                const int tc = t < len ? t : len - 1;
-                const uint16_t *row = qp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + 32 * s;
-                qraw[ii][q4][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
-                qraw[ii][q4][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
-            }
+        for (int q2 = 0; q2 < 2; ++q2) {
+            const int s = 2 * sh + q2;
+            const int tc = t < len ? t : len - 1;
+            const uint16_t *row = qp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + 32 * s;
+            qraw[ii][q2][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
+            qraw[ii][q2][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
         }
     }
     // padding rows of q are zeroed (loaded from a row clamped into the chunk)
@@ -347,21 +347,32 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     for (int ii = 0; ii < 2; ++ii) {
         const uint32_t keep = keep_mask(16 * (ii == 0 ? IA : 3 - IA) + r < len);
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            qraw[ii][q4][0].x &= keep;
-            qraw[ii][q4][0].y &= keep;
-            qraw[ii][q4][1].x &= keep;
-            qraw[ii][q4][1].y &= keep;
+        for (int q2 = 0; q2 < 2; ++q2) {
+            qraw[ii][q2][0].x &= keep;
+            qraw[ii][q2][0].y &= keep;
+            qraw[ii][q2][1].x &= keep;
+            qraw[ii][q2][1].y &= keep;
         }
     }
+    // widened q: 8 channels {32s + kperm(gq, e)} of slice s = 2 sh + q2
+    auto q8 = [&](int ii, int q2, float x[8]) {
+        const uint2 q0 = qraw[ii][q2][0];
+        const uint2 q1 = qraw[ii][q2][1];
+        x[0] = __uint_as_float(q0.x << 16);
+        x[1] = __uint_as_float(q0.x & 0xffff0000u);
+        x[2] = __uint_as_float(q0.y << 16);
+        x[3] = __uint_as_float(q0.y & 0xffff0000u);
+        x[4] = __uint_as_float(q1.x << 16);
+        x[5] = __uint_as_float(q1.x & 0xffff0000u);
+        x[6] = __uint_as_float(q1.y << 16);
+        x[7] = __uint_as_float(q1.y & 0xffff0000u);
+    };
 
     // ---- S1: k rows, log2 decay, beta, v (zero-padded) ---------------------
     const int kc = tid & 31;
     const int rg = tid >> 5;
-    uint2 vraw[8];  // v rows rg + 8i, columns 4kc..4kc+3 (written to LDS after S4)
     {
         const uint16_t *kp = static_cast<const uint16_t *>(a.k);
-        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
         float expA = 0.f;
         float4 dtb = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (GATE == KDA_GATE_RAW) {
@@ -386,7 +397,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             const int tc = t < len ? t : len - 1;
             const int64_t base = (static_cast<int64_t>(t0 + tc) * H + h) * DK + 4 * kc;
             kraw[i] = *reinterpret_cast<const uint2 *>(kp + base);
-            vraw[i] = *reinterpret_cast<const uint2 *>(vp + base);
             if constexpr (GATE == KDA_GATE_RAW) {
                 g4[i] = load4(static_cast<const uint16_t *>(a.gate) + base);
             } else {
@@ -398,8 +408,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             const uint32_t keep = keep_mask(rg + 8 * i < len);
             kraw[i].x &= keep;
             kraw[i].y &= keep;
-            vraw[i].x &= keep;
-            vraw[i].y &= keep;
             if constexpr (GATE == KDA_GATE_RAW) {
                 const float4 av = g4[i];
                 const float lb = a.lower_bound;
@@ -428,8 +436,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             } else if (kc == 0) {
                 sm.rnk[t] = 1.0f;
             }
-            *reinterpret_cast<uint2 *>(&sm.r1.K[t][4 * kc]) = kraw[i];
-            *reinterpret_cast<float4 *>(&sm.r0.G[t][4 * kc]) =
+            *reinterpret_cast<uint2 *>(&sm.u.early.K[t][4 * kc]) = kraw[i];
+            *reinterpret_cast<float4 *>(&sm.u.early.G[t][4 * kc]) =
                 make_float4(g4[i].x * kLog2e, g4[i].y * kLog2e, g4[i].z * kLog2e, g4[i].w * kLog2e);
         }
         if (tid < BT) {
@@ -438,6 +446,28 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 b = 1.0f / (1.0f + __expf(-b));
             }
             sm.beta[tid] = tid < len ? b : 0.f;
+        }
+    }
+    if (norm) {
+        // this wave's half of each q row's sum of squares (4 lane groups x
+        // 2 slices), one lane per row writes it
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            float x[8];
+            float ss = 0.f;
+#pragma unroll
+            for (int q2 = 0; q2 < 2; ++q2) {
+                q8(ii, q2, x);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    ss += x[e] * x[e];
+                }
+            }
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (gq == 0) {
+                sm.u.early.qss[sh][16 * (ii == 0 ? IA : 3 - IA) + r] = ss;
+            }
         }
     }
     lds_barrier();
@@ -450,7 +480,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         float run = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            run += sm.r0.G[half * 32 + i][ch];
+            run += sm.u.early.G[half * 32 + i][ch];
             vals[i] = run;
         }
         if (half == 0) {
@@ -460,19 +490,19 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         const float add = half ? sm.carry[ch] : 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            sm.r0.G[half * 32 + i][ch] = vals[i] + add;
+            sm.u.early.G[half * 32 + i][ch] = vals[i] + add;
         }
     }
     lds_barrier();
 
     auto kval = [&](int t, int k) {
-        return bf16_to_f32(sm.r1.K[t][k]) * sm.rnk[t];
+        return bf16_to_f32(sm.u.early.K[t][k]) * sm.rnk[t];
     };
     // 8 channels {32s + kperm(gq, e)} of one row: two 8-byte k reads, two
     // 16-byte G reads.
     auto load_k8 = [&](int row, int s, float x[8]) {
-        const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.r1.K[row][32 * s + 4 * gq]);
-        const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.r1.K[row][32 * s + 16 + 4 * gq]);
+        const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.u.early.K[row][32 * s + 4 * gq]);
+        const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.u.early.K[row][32 * s + 16 + 4 * gq]);
         x[0] = __uint_as_float(k0.x << 16);
         x[1] = __uint_as_float(k0.x & 0xffff0000u);
         x[2] = __uint_as_float(k0.y << 16);
@@ -483,8 +513,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         x[7] = __uint_as_float(k1.y & 0xffff0000u);
     };
     auto load_g8 = [&](int row, int s, float x[8]) {
-        const float4 g0 = *reinterpret_cast<const float4 *>(&sm.r0.G[row][32 * s + 4 * gq]);
-        const float4 g1 = *reinterpret_cast<const float4 *>(&sm.r0.G[row][32 * s + 16 + 4 * gq]);
+        const float4 g0 = *reinterpret_cast<const float4 *>(&sm.u.early.G[row][32 * s + 4 * gq]);
+        const float4 g1 = *reinterpret_cast<const float4 *>(&sm.u.early.G[row][32 * s + 16 + 4 * gq]);
         x[0] = g0.x;
         x[1] = g0.y;
         x[2] = g0.z;
@@ -496,51 +526,22 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     };
 
     // ---- S3: Akk (-> L^T), Aqk (-> LT's lower triangle), q e^G fragments ----
-    // Half sh = 1 stores its partial products into LT; after a barrier half
-    // sh = 0 adds its own (held in registers) and applies beta. Every LT
-    // element is written: block (J, I), J < I, holds Akk^T; block (I, J),
-    // J < I, holds Aqk; a diagonal block holds Akk^T above and Aqk on and
-    // below its diagonal.
-    f32x4 pk[2][4], pq[2][4];  // sh = 0 partials of pair (I, J): Akk, Aqk
+    // Each wave sums its pairs over its channel half; the partial products
+    // stay in registers until the k and cumsum tiles are dead (after S4), and
+    // the halves are then summed in LT.
+    f32x4 pk[2][4], pq[2][4];  // this half's partials of pair (I, J): Akk, Aqk
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
         const int I = ii == 0 ? IA : 3 - IA;
         const int ri = 16 * I + r;
-        // q row: widen this half's channels, norm over all 128 (4 lane groups
-        // x 4 slices), scale
+        // q row: this half's channels, scaled by the norm over all 128
+        // (the two halves' sums of squares meet in LDS during S1)
         float qv[2][8];
-        float qss = 0.f;
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const uint2 q0 = qraw[ii][q4][0];
-            const uint2 q1 = qraw[ii][q4][1];
-            float x[8];
-            x[0] = __uint_as_float(q0.x << 16);
-            x[1] = __uint_as_float(q0.x & 0xffff0000u);
-            x[2] = __uint_as_float(q0.y << 16);
-            x[3] = __uint_as_float(q0.y & 0xffff0000u);
-            x[4] = __uint_as_float(q1.x << 16);
-            x[5] = __uint_as_float(q1.x & 0xffff0000u);
-            x[6] = __uint_as_float(q1.y << 16);
-            x[7] = __uint_as_float(q1.y & 0xffff0000u);
-            if (q4 < 2) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    qv[q4][e] = x[e];
-                }
-            }
-            if (norm) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    qss += x[e] * x[e];
-                }
-            }
-        }
+        q8(ii, 0, qv[0]);
+        q8(ii, 1, qv[1]);
         float qscale = a.scale;
         if (norm) {
-            qss += __shfl_xor(qss, 16);
-            qss += __shfl_xor(qss, 32);
-            qscale = a.scale / sqrtf(qss + 1e-6f);
+            qscale = a.scale / sqrtf(sm.u.early.qss[0][ri] + sm.u.early.qss[1][ri] + 1e-6f);
         }
         // the block's anchor row G[16I][.]
         float anc[2][8];
@@ -598,21 +599,139 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 aqt = mfma(Ch, Ql[sl], aqt);
                 aqt = mfma(Cl, Qh[sl], aqt);
             }
-            if (sh == 0) {
-                pk[ii][J] = akk;
-                pq[ii][J] = aqt;
-            } else if (J < I) {
-                // lane (r, gq) holds Akk[16I + 4gq + e][16J + r] and Aqk[16I + r][16J + 4gq + e]
-                *reinterpret_cast<f32x4 *>(&sm.LT[16 * J + r][16 * I + 4 * gq]) = akk;
-                *reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * J + 4 * gq]) = aqt;
-            } else {
-                f32x4 m;
+            // lane (r, gq) holds Akk[16I + 4gq + e][16J + r] and Aqk[16I + r][16J + 4gq + e]
+            pk[ii][J] = akk;
+            pq[ii][J] = aqt;
+        }
+    }
+
+    // ---- S4: kd^T fragments, e^(G_last), tracking operands, e^G k ----------
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    m[e] = r < 4 * gq + e ? akk[e] : aqt[e];
-                }
-                *reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * I + 4 * gq]) = m;
+    for (int tt = 0; tt < 2; ++tt) {
+        const int mk = 2 * wave + tt;
+        const int k = 16 * mk + r;
+        const float gl = sm.u.early.G[BT - 1][k];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = 32 * s + kperm(gq, e);
+                x[e] = kval(t, k) * ex2(gl - sm.u.early.G[t][k]);
             }
+            bf16x8 fh, fl;
+            split_bf16x8(x, fh, fl);
+            store_frag(rec, kOffKdH, mk * 2 + s, lane, fh);
+            store_frag(rec, kOffKdL, mk * 2 + s, lane, fl);
+        }
+    }
+    if (tid < DK) {
+        reinterpret_cast<float *>(rec + kOffGl)[tid] = ex2(sm.u.early.G[BT - 1][tid]);
+    }
+    // The tracked prefix inside this chunk (0 < rr < len): its state is
+    // e^(G_{rr-1}) S + (e^(G_{rr-1} - G_t) k_t)_{t<rr}^T vnew.
+    if (a.track_indices != nullptr) {
+        const int ts = a.track_indices[n];
+        const int tl = a.track_lens[n];
+        const int rr = tl - BT * jc;
+        if (ts > 0 && static_cast<int64_t>(ts) < a.num_slots && rr > 0 && rr < len) {
+            char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int mk = 2 * wave + tt;
+                const int k = 16 * mk + r;
+                const float gr = sm.u.early.G[rr - 1][k];
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    float x[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int t = 32 * s + kperm(gq, e);
+                        x[e] = t < rr ? kval(t, k) * ex2(gr - sm.u.early.G[t][k]) : 0.f;
+                    }
+                    bf16x8 fh, fl;
+                    split_bf16x8(x, fh, fl);
+                    store_frag(tr, kTrOffKdH, mk * 2 + s, lane, fh);
+                    store_frag(tr, kTrOffKdL, mk * 2 + s, lane, fl);
+                }
+            }
+            if (tid < DK) {
+                reinterpret_cast<float *>(tr + kTrOffGl)[tid] = ex2(sm.u.early.G[rr - 1][tid]);
+            }
+        }
+    }
+    // e^G k rows rg + 8i, columns 4kc..4kc+3, as bf16 (written after the barrier)
+    uint2 kep[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int t = rg + 8 * i;
+        const uint2 k2 = *reinterpret_cast<const uint2 *>(&sm.u.early.K[t][4 * kc]);
+        const float4 g4 = *reinterpret_cast<const float4 *>(&sm.u.early.G[t][4 * kc]);
+        const float rn = sm.rnk[t];
+        kep[i].x = pack_bf16x2(__uint_as_float(k2.x << 16) * rn * ex2(g4.x),
+                               __uint_as_float(k2.x & 0xffff0000u) * rn * ex2(g4.y));
+        kep[i].y = pack_bf16x2(__uint_as_float(k2.y << 16) * rn * ex2(g4.z),
+                               __uint_as_float(k2.y & 0xffff0000u) * rn * ex2(g4.w));
+    }
+    lds_barrier();  // G and K are dead from here on
+    // v rows rg + 8i, columns 4kc..4kc+3, loaded now (their latency hides
+    // behind S5) and written to LDS in S6, over X and LT
+    uint2 vraw[8];
+    {
+        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int t = rg + 8 * i;
+            const int tc = t < len ? t : len - 1;
+            vraw[i] = *reinterpret_cast<const uint2 *>(
+                vp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + 4 * kc);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t keep = keep_mask(rg + 8 * i < len);
+            vraw[i].x &= keep;
+            vraw[i].y &= keep;
+        }
+    }
+    // S3's two channel halves meet in LT, which lies over the dead G: half
+    // sh = 1 stores its partial products, then half sh = 0 adds its own and
+    // applies beta. Every LT element is written: block (J, I), J < I, holds
+    // Akk^T; block (I, J), J < I, holds Aqk; a diagonal block holds Akk^T
+    // above and Aqk on and below its diagonal.
+    if (sh == 1) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const int I = ii == 0 ? IA : 3 - IA;
+#pragma unroll
+            for (int J = 0; J < (ii == 0 ? 4 : 2); ++J) {
+                if (J > I) {
+                    break;
+                }
+                if (J < I) {
+                    *reinterpret_cast<f32x4 *>(&sm.u.mid.LT[16 * J + r][16 * I + 4 * gq]) = pk[ii][J];
+                    *reinterpret_cast<f32x4 *>(&sm.u.mid.LT[16 * I + r][16 * J + 4 * gq]) = pq[ii][J];
+                } else {
+                    f32x4 m;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        m[e] = r < 4 * gq + e ? pk[ii][J][e] : pq[ii][J][e];
+                    }
+                    *reinterpret_cast<f32x4 *>(&sm.u.mid.LT[16 * I + r][16 * I + 4 * gq]) = m;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int t = rg + 8 * i;
+        *reinterpret_cast<uint2 *>(&sm.u.mid.KE[t][4 * kc]) = kep[i];
+    }
+    // X: upper blocks zero
+    for (int idx = tid; idx < BT * BT; idx += kThreads) {
+        const int i = idx >> 6;
+        const int j = idx & 63;
+        if ((j >> 4) > (i >> 4)) {
+            sm.u.mid.X[i][j] = 0.f;
         }
     }
     lds_barrier();
@@ -628,14 +747,14 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                     break;
                 }
                 if (J < I) {
-                    f32x4 *pa = reinterpret_cast<f32x4 *>(&sm.LT[16 * J + r][16 * I + 4 * gq]);
-                    f32x4 *pb = reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * J + 4 * gq]);
+                    f32x4 *pa = reinterpret_cast<f32x4 *>(&sm.u.mid.LT[16 * J + r][16 * I + 4 * gq]);
+                    f32x4 *pb = reinterpret_cast<f32x4 *>(&sm.u.mid.LT[16 * I + r][16 * J + 4 * gq]);
                     const f32x4 xa = *pa;
                     const f32x4 xb = *pb;
                     *pa = (xa + pk[ii][J]) * bv;
                     *pb = xb + pq[ii][J];
                 } else {
-                    f32x4 *pd = reinterpret_cast<f32x4 *>(&sm.LT[16 * I + r][16 * I + 4 * gq]);
+                    f32x4 *pd = reinterpret_cast<f32x4 *>(&sm.u.mid.LT[16 * I + r][16 * I + 4 * gq]);
                     const f32x4 xd = *pd;
                     f32x4 m;
 #pragma unroll
@@ -647,92 +766,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             }
         }
     }
-
-
-    // ---- S4: kd^T fragments, e^(G_last), tracking operands, e^G k ----------
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int mk = 2 * wave + tt;
-        const int k = 16 * mk + r;
-        const float gl = sm.r0.G[BT - 1][k];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            float x[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int t = 32 * s + kperm(gq, e);
-                x[e] = kval(t, k) * ex2(gl - sm.r0.G[t][k]);
-            }
-            bf16x8 fh, fl;
-            split_bf16x8(x, fh, fl);
-            store_frag(rec, kOffKdH, mk * 2 + s, lane, fh);
-            store_frag(rec, kOffKdL, mk * 2 + s, lane, fl);
-        }
-    }
-    if (tid < DK) {
-        reinterpret_cast<float *>(rec + kOffGl)[tid] = ex2(sm.r0.G[BT - 1][tid]);
-    }
-    // The tracked prefix inside this chunk (0 < rr < len): its state is
-    // e^(G_{rr-1}) S + (e^(G_{rr-1} - G_t) k_t)_{t<rr}^T vnew.
-    if (a.track_indices != nullptr) {
-        const int ts = a.track_indices[n];
-        const int tl = a.track_lens[n];
-        const int rr = tl - BT * jc;
-        if (ts > 0 && static_cast<int64_t>(ts) < a.num_slots && rr > 0 && rr < len) {
-            char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const int mk = 2 * wave + tt;
-                const int k = 16 * mk + r;
-                const float gr = sm.r0.G[rr - 1][k];
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    float x[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int t = 32 * s + kperm(gq, e);
-                        x[e] = t < rr ? kval(t, k) * ex2(gr - sm.r0.G[t][k]) : 0.f;
-                    }
-                    bf16x8 fh, fl;
-                    split_bf16x8(x, fh, fl);
-                    store_frag(tr, kTrOffKdH, mk * 2 + s, lane, fh);
-                    store_frag(tr, kTrOffKdL, mk * 2 + s, lane, fl);
-                }
-            }
-            if (tid < DK) {
-                reinterpret_cast<float *>(tr + kTrOffGl)[tid] = ex2(sm.r0.G[rr - 1][tid]);
-            }
-        }
-    }
-    // e^G k rows rg + 8i, columns 4kc..4kc+3, as bf16 (written after the barrier)
-    uint2 kep[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int t = rg + 8 * i;
-        const uint2 k2 = *reinterpret_cast<const uint2 *>(&sm.r1.K[t][4 * kc]);
-        const float4 g4 = *reinterpret_cast<const float4 *>(&sm.r0.G[t][4 * kc]);
-        const float rn = sm.rnk[t];
-        kep[i].x = pack_bf16x2(__uint_as_float(k2.x << 16) * rn * ex2(g4.x),
-                               __uint_as_float(k2.x & 0xffff0000u) * rn * ex2(g4.y));
-        kep[i].y = pack_bf16x2(__uint_as_float(k2.y << 16) * rn * ex2(g4.z),
-                               __uint_as_float(k2.y & 0xffff0000u) * rn * ex2(g4.w));
-    }
-    lds_barrier();  // G and K are dead from here on
+    lds_barrier();
     {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int t = rg + 8 * i;
-            *reinterpret_cast<uint2 *>(&sm.r1.KE[t][4 * kc]) = kep[i];
-            *reinterpret_cast<uint2 *>(&sm.r0.late.V[t][4 * kc]) = vraw[i];
-        }
-        // X: upper blocks zero
-        for (int idx = tid; idx < BT * BT; idx += kThreads) {
-            const int i = idx >> 6;
-            const int j = idx & 63;
-            if ((j >> 4) > (i >> 4)) {
-                sm.r0.late.X[i][j] = 0.f;
-            }
-        }
         // Aqk fragments (mt = wave, s): rows 16 wave + r, zero above the diagonal
         const int row = 16 * wave + r;
 #pragma unroll
@@ -740,8 +775,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             if (s == 1 && wave < 2) {
                 break;  // an all-zero fragment (uniform per wave)
             }
-            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.LT[row][32 * s + 4 * gq]);
-            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.LT[row][32 * s + 16 + 4 * gq]);
+            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 4 * gq]);
+            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 16 + 4 * gq]);
             const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             float x[8];
 #pragma unroll
@@ -775,7 +810,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             float lrow[16];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float4 t4 = *reinterpret_cast<const float4 *>(&sm.LT[b0 + j][b0 + 4 * q]);
+                const float4 t4 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[b0 + j][b0 + 4 * q]);
                 lrow[4 * q + 0] = t4.x;
                 lrow[4 * q + 1] = t4.y;
                 lrow[4 * q + 2] = t4.z;
@@ -790,7 +825,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            sm.r0.late.X[b0 + i][b0 + col] = acc[i];
+            sm.u.mid.X[b0 + i][b0 + col] = acc[i];
         }
     }
     lds_barrier();
@@ -809,28 +844,28 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 #pragma unroll
                 for (int k4 = 0; k4 < 4; ++k4) {
                     const int kk = 16 * K + 4 * k4 + gq;
-                    m = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.LT[kk][16 * I + r],
-                                                            sm.r0.late.X[kk][16 * J + r], m, 0, 0, 0);
+                    m = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.u.mid.LT[kk][16 * I + r],
+                                                            sm.u.mid.X[kk][16 * J + r], m, 0, 0, 0);
                 }
             }
             // lane (r, gq) holds M[4gq + i][r]; park it row-major in block (J, I)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                sm.r0.late.X[16 * J + 4 * gq + i][16 * I + r] = m[i];
+                sm.u.mid.X[16 * J + 4 * gq + i][16 * I + r] = m[i];
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             f32x4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k4 = 0; k4 < 4; ++k4) {
-                x = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.r0.late.X[16 * I + r][16 * I + 4 * k4 + gq],
-                                                        sm.r0.late.X[16 * J + 4 * k4 + gq][16 * I + r], x,
+                x = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.u.mid.X[16 * I + r][16 * I + 4 * k4 + gq],
+                                                        sm.u.mid.X[16 * J + 4 * k4 + gq][16 * I + r], x,
                                                         0, 0, 0);
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                sm.r0.late.X[16 * I + 4 * gq + i][16 * J + r] = -x[i];
-                sm.r0.late.X[16 * J + 4 * gq + i][16 * I + r] = 0.f;
+                sm.u.mid.X[16 * I + 4 * gq + i][16 * J + r] = -x[i];
+                sm.u.mid.X[16 * J + 4 * gq + i][16 * I + r] = 0.f;
             }
         }
         lds_barrier();
@@ -838,7 +873,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     for (int idx = tid; idx < BT * BT; idx += kThreads) {
         const int i = idx >> 6;
         const int j = idx & 63;
-        sm.r0.late.X[i][j] *= sm.beta[j];
+        sm.u.mid.X[i][j] *= sm.beta[j];
     }
     lds_barrier();
 
@@ -849,11 +884,18 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         bf16x8 Th[2], Tl[2];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.r0.late.X[t][32 * s + 4 * gq]);
-            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.r0.late.X[t][32 * s + 16 + 4 * gq]);
+            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.u.mid.X[t][32 * s + 4 * gq]);
+            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.u.mid.X[t][32 * s + 16 + 4 * gq]);
             const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             split_bf16x8(x, Th[s], Tl[s]);
         }
+        // v goes over the dead X and LT once every wave holds its T rows
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            *reinterpret_cast<uint2 *>(&sm.u.late.V[rg + 8 * i][4 * kc]) = vraw[i];
+        }
+        lds_barrier();
         // u tiles (mt = wave, vt): A = T rows, B = v (K = token)
 #pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
@@ -863,7 +905,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 if (s >= nS) {
                     break;  // uniform per wave; keeps s (and Th[s]) static
                 }
-                const bf16x8 vb = lds_tr_frag(&sm.r0.late.V[0][0], 32 * s, 16 * vt, lane);
+                const bf16x8 vb = lds_tr_frag(&sm.u.late.V[0][0], 32 * s, 16 * vt, lane);
                 acc = mfma(Th[s], vb, acc);
                 acc = mfma(Tl[s], vb, acc);
             }
@@ -882,7 +924,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                     if (s >= nS) {
                         break;
                     }
-                    const bf16x8 kb = lds_tr_frag(&sm.r1.KE[0][0], 32 * s, 16 * mk, lane);
+                    const bf16x8 kb = lds_tr_frag(&sm.u.mid.KE[0][0], 32 * s, 16 * mk, lane);
                     acc = mfma(kb, Th[s], acc);
                 }
                 // acc[i] = w[16*wave + r][16*mk + 4gq + i]
