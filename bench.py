@@ -55,12 +55,12 @@ DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
 # The kernel-trace/PMC summaries are kept under profiles/.
 FETCH_SCALE = 524288.0 / 262156.8
 WRITE_SCALE = 524288.0 / 524288.0
-DEC_FETCH_KIB, DEC_WRITE_KIB = 267451.4, 526336.2
+DEC_FETCH_KIB, DEC_WRITE_KIB = 267449.1, 526336.1
 DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
 # Same for config 5's 4-token verify launch (1024 sequences, H=16).
 VF_TRAFFIC = (565882.7 * FETCH_SCALE + 1063961.9 * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
-PF_TRAFFIC = ((168219.6 + 261478.4) * FETCH_SCALE + (509952.0 + 108790.8) * WRITE_SCALE) * 1024
+PF_TRAFFIC = ((168207.2 + 263951.0) * FETCH_SCALE + (509952.0 + 107667.9) * WRITE_SCALE) * 1024
 # MFMA counters of the same two kernels (profiles/prefill_chunk_t8192_h32_mfma.md): matrix work
 # executed per call (SQ_INSTS_VALU_MFMA_MOPS_* x 512 FLOP; the hi/lo operand splits roughly
 # double the algorithmic count) and the fraction of SIMD cycles each kernel keeps the MFMA busy.
