@@ -159,6 +159,34 @@ def test_prepared_chunk_matches_oracle_small(gpu_ops):
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
 
 
+def test_prepared_chunk_many_sequences(gpu_ops):
+    """More sequences than the chunk-index kernel has threads (1500 > 1024, so
+    each thread sums several sequences' chunk counts): short ragged and empty
+    sequences, some on the padding slot 0, against the oracle; unused slots
+    byte-identical."""
+    import random
+
+    rng = random.Random(5)
+    n = 1500
+    lengths = [rng.choice([0, 1, 63, 64, 65]) if rng.random() < 0.3 else rng.randint(1, 70)
+               for _ in range(n)]
+    slots = n + 40
+    indices = [0 if rng.random() < 0.05 else s for s in rng.sample(range(1, slots), n)]
+    case = C.prepared_case(2, lengths, slots=slots, indices=indices, seed=77)
+    dev = _prepared_dev(case)
+    pool = C.to_dev(case.pool, DEV)
+    out = _chunk_prepared(gpu_ops, case, pool, dev)
+    ref_pool = C.clone_pool(case.pool)
+    ref = R.kda_chunk(case.q.float() * case.scale, case.k, case.v, case.g, case.beta,
+                      state_pool=ref_pool, state_indices=case.indices,
+                      cu_seqlens=case.cu_seqlens, out_dtype=torch.float32)
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, "output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
+    used = set(s for s in indices if s > 0)
+    other = [s for s in range(slots) if s not in used]
+    assert torch.equal(pool.cpu()[other], case.pool[other]), "an unused slot was written"
+
+
 @pytest.mark.parametrize(
     "name,heads,lengths,slots,indices,gate",
     [
