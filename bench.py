@@ -370,7 +370,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
-              "(the KDA path shards by head and sequence with no exchange; see DESIGN.md).",
+              "(the KDA path shards by head and sequence with no exchange inside the op).",
               file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"

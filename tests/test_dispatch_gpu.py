@@ -1,5 +1,5 @@
-"""The op-then-fallback dispatcher with the native op on the GPU (SURVEY row f4;
-reference: tests/integration/kda_ascendc_dispatch.py:64-87).
+"""The op-then-fallback dispatcher with the native op on the GPU (the
+reference's tests/integration/kda_ascendc_dispatch.py:64-87).
 
 A K-contiguous pool takes the native path and matches the oracle; a plain
 [slots, H, K, V]-contiguous pool is one of the op's deliberate rejections

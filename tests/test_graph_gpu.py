@@ -1,7 +1,7 @@
 """HIP-graph capture and replay with metadata mutated behind the captured pointers.
 
 Mirrors the reference's graph check (tests/integration/
-test_glm53_kda_prefix_ascendc.py:185-293; SURVEY row f4): one op call is
+test_glm53_kda_prefix_ascendc.py:185-293): one op call is
 captured, then replayed eight times. Before every replay the slot indices
 (including the padding slot 0), the packed sequence boundaries and the
 tracking slots/lengths are rewritten in place, the inputs get fresh values and

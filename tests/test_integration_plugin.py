@@ -1,5 +1,5 @@
 """sglang integration pieces on the CPU: the plugin hook and the op-then-fallback
-dispatcher (SURVEY row f4; reference: src/sgl_glm53_ascend_ops/plugin.py:1-36,
+dispatcher (reference: src/sgl_glm53_ascend_ops/plugin.py:1-36,
 tests/integration/kda_ascendc_dispatch.py:52-101).
 
 sglang is not installed, so its ``HookRegistry`` is replaced by a recording
