@@ -123,7 +123,11 @@ typedef struct KdaRecurrentArgs {
     int32_t qk_l2norm; /* LOG mode: normalize q and k in the kernel */
 } KdaRecurrentArgs;
 
-/* Fused recurrent (token-by-token) KDA over packed varlen sequences. */
+/* Fused recurrent (token-by-token) KDA over packed varlen sequences.
+ * Alignment (KDA_ERR_INVALID_ARGUMENT otherwise): state and intermediate
+ * bases 16 bytes with strides that are multiples of 4 elements; q and k 8
+ * bytes (bf16) or 16 (fp32); gate 8 bytes (RAW) or 16. v and out may sit
+ * anywhere: aligned ones move as vectors, others element by element. */
 int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream);
 
 typedef struct KdaChunkArgs {
