@@ -1472,9 +1472,11 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     if (a.num_seqs == 0) {
         return KDA_OK;
     }
-    if (a.q == nullptr || a.k == nullptr || a.v == nullptr || a.gate == nullptr ||
-        a.beta == nullptr || a.state == nullptr || a.state_indices == nullptr ||
-        a.cu_seqlens == nullptr || a.out == nullptr) {
+    // token tensors are never read or written when there are no tokens
+    const bool tokens = a.num_tokens > 0;
+    if ((tokens && (a.q == nullptr || a.k == nullptr || a.v == nullptr || a.gate == nullptr ||
+                    a.beta == nullptr || a.out == nullptr)) ||
+        a.state == nullptr || a.state_indices == nullptr || a.cu_seqlens == nullptr) {
         return KDA_ERR_INVALID_ARGUMENT;
     }
     if (a.gate_mode == KDA_GATE_RAW && (a.A_log == nullptr || a.dt_bias == nullptr)) {

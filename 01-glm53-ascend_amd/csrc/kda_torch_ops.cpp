@@ -230,7 +230,10 @@ at::Tensor varlen_recurrent_impl(const char *op, const at::Tensor &A_log, const 
     // output needs no fill: the reference's zeros_like is kept as a contract,
     // not as a memset.
     at::Tensor out = at::empty_like(v);
-    if (N == 0 || T == 0) {
+    // No request: every token is uncovered, so zero. No tokens but some
+    // requests still launch: a prefix tracked at length 0 receives the
+    // request's initial state.
+    if (N == 0) {
         return out.zero_();
     }
     const PoolRef pr = pool_ref(pool);
@@ -364,7 +367,10 @@ at::Tensor varlen_chunk_impl(const char *op, const at::Tensor &A_log, const at::
     const auto ti32 = as_int32_opt(track_indices);
     const auto tl32 = as_int32_opt(track_lens);
     at::Tensor out = at::empty_like(v);
-    if (N == 0 || T == 0) {
+    // No request: every token is uncovered, so zero. No tokens but some
+    // requests still launch: a prefix tracked at length 0 receives the
+    // request's initial state.
+    if (N == 0) {
         return out.zero_();
     }
     const PoolRef pr = pool_ref(pool);
@@ -511,7 +517,10 @@ at::Tensor kda_prepared_varlen_recurrent(const at::Tensor &q, const at::Tensor &
     const auto ti32 = as_int32_opt(track_state_indices);
     const auto tl32 = as_int32_opt(track_state_lens);
     at::Tensor out = at::empty_like(v);
-    if (N == 0 || p.T == 0) {
+    // No request: every token is uncovered, so zero. No tokens but some
+    // requests still launch: a prefix tracked at length 0 receives the
+    // request's initial state.
+    if (N == 0) {
         return out.zero_();
     }
     const PoolRef pr = pool_ref(initial_state_source);
@@ -577,7 +586,10 @@ at::Tensor kda_prepared_varlen_chunk(const at::Tensor &q, const at::Tensor &k,
     const auto ti32 = as_int32_opt(track_state_indices);
     const auto tl32 = as_int32_opt(track_state_lens);
     at::Tensor out = at::empty_like(v);
-    if (N == 0 || p.T == 0) {
+    // No request: every token is uncovered, so zero. No tokens but some
+    // requests still launch: a prefix tracked at length 0 receives the
+    // request's initial state.
+    if (N == 0) {
         return out.zero_();
     }
     const PoolRef pr = pool_ref(initial_state_source);
@@ -687,7 +699,7 @@ void prepared_recurrent(const at::Tensor &qn, const at::Tensor &kn, const at::Te
     check_on_gpu("kn", kn);
     check_on_gpu("v", v);
     const c10::DeviceGuard device_guard(qn.device());  // launch on qn's device
-    if (N == 0 || T == 0) {
+    if (N == 0) {  // no tokens but some requests still launch (tracking at length 0)
         return;
     }
     // The reference pool for this op is [K,V]-contiguous; the native pool of

@@ -33,6 +33,10 @@
  *   indices         int32 [N]; entries outside [0, num_slots) are treated as
  *                   slot 0 (the kernels never address outside the pool).
  *
+ * With num_tokens == 0 the token pointers (q, k, v, gate, beta, out) may be
+ * null: the requests still run, so a prefix tracked at length 0 receives the
+ * request's initial state.
+ *
  * All launches are asynchronous on `stream` and never synchronize the host.
  * Every function returns a KdaStatus (0 = success).
  */

@@ -167,6 +167,9 @@ def prepared_case(heads: int, lengths: Sequence[int], *, D: int = 128, dtype=tor
 def max_rel_err(x: torch.Tensor, ref: torch.Tensor) -> float:
     x = x.detach().double().cpu()
     ref = ref.detach().double().cpu()
+    assert x.shape == ref.shape, f"shape {tuple(x.shape)} != {tuple(ref.shape)}"
+    if ref.numel() == 0:  # an empty batch (no tokens) has nothing to compare
+        return 0.0
     den = ref.abs().max().item()
     num = (x - ref).abs().max().item()
     return num if den == 0.0 else num / den
@@ -186,6 +189,9 @@ def out_err(x: torch.Tensor, ref: torch.Tensor) -> float:
         return max_rel_err(x, ref)
     xd = x.detach().double().cpu()
     rd = ref.detach().double().cpu()
+    assert xd.shape == rd.shape, f"shape {tuple(xd.shape)} != {tuple(rd.shape)}"
+    if rd.numel() == 0:
+        return 0.0
     den = rd.abs().max().item()
     beyond = ((xd - rd).abs() - half_ulp_bf16(x)).clamp_min(0).max().item()
     return beyond if den == 0.0 else beyond / den

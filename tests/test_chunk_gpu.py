@@ -215,3 +215,20 @@ def test_baseline_configs_chunk_vs_recurrent(gpu_ops, name, heads, lengths, slot
     e_s = C.assert_rel(pool_c.cpu(), pool_r.cpu(), C.STATE_TOL, f"{name} final states")
     print(f"{name}: output err {e_o:.2e}, state err {e_s:.2e}")
     assert torch.isfinite(out_c.float()).all()
+
+
+def test_chunk_no_tokens_tracks_initial_state(gpu_ops):
+    """An empty batch (two requests, no tokens) still runs the requests: the
+    prefix tracked at length 0 receives the request's initial state, the
+    source slots are rewritten unchanged and nothing else moves
+    (kda_python.py:168-179 semantics, as the oracle)."""
+    case = C.raw_case(4, (0, 0), indices=[2, 0], slots=6, seed=91, track=([4, 5], [0, 0]))
+    pool = C.to_dev(case.pool, DEV)
+    out = gpu_ops.kda_varlen_chunk(prefill=True, **case.kwargs(DEV, pool=pool))
+    torch.cuda.synchronize()
+    assert out.shape == case.v.shape and out.numel() == 0
+    got = pool.cpu()
+    assert torch.equal(got[4], case.pool[2]), "tracked slot 4 must hold slot 2's state"
+    assert torch.equal(got[5], torch.zeros_like(got[5])), "slot-0 request tracks a zero state"
+    for s in (0, 1, 2, 3):
+        assert torch.equal(got[s], case.pool[s]), f"slot {s} changed"

@@ -478,3 +478,15 @@ def test_config5_decode_full_size(gpu_ops):
         e_s = max(e_s, C.assert_rel(pool[int(perm[s])].cpu(), ref_pool[1], C.STATE_TOL,
                                     f"sequence {s} state"))
     print(f"config5 decode: output err {e_o:.2e}, state err {e_s:.2e}")
+
+
+def test_recurrent_no_tokens_tracks_initial_state(gpu_ops):
+    """The recurrent op's empty batch: as the chunk op's (prefill mode)."""
+    case = C.raw_case(4, (0, 0), indices=[2, 0], slots=6, seed=92, track=([4, 5], [0, 0]))
+    out, pool = _run_raw(gpu_ops, case, prefill=True)
+    assert out.shape == case.v.shape and out.numel() == 0
+    got = pool.cpu()
+    assert torch.equal(got[4], case.pool[2]), "tracked slot 4 must hold slot 2's state"
+    assert torch.equal(got[5], torch.zeros_like(got[5])), "slot-0 request tracks a zero state"
+    for s in (0, 1, 2, 3):
+        assert torch.equal(got[s], case.pool[s]), f"slot {s} changed"

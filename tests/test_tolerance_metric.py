@@ -26,3 +26,15 @@ def test_fp32_outputs_use_the_plain_metric():
     ref = torch.randn(100, generator=C.gen(3), dtype=torch.float64)
     x = ref.float()
     assert C.out_err(x, ref) == C.max_rel_err(x, ref) < 1e-6
+
+
+def test_empty_batches_compare_equal_and_shapes_must_match():
+    empty = torch.zeros(1, 0, 4, 128)
+    assert C.max_rel_err(empty, empty.double()) == 0.0
+    assert C.out_err(empty.bfloat16(), empty.double()) == 0.0
+    try:
+        C.max_rel_err(torch.zeros(3), torch.zeros(4))
+    except AssertionError:
+        pass
+    else:
+        raise AssertionError("a shape mismatch must not pass")
