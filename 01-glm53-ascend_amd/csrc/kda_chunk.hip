@@ -290,23 +290,33 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     const int h = static_cast<int>(blockIdx.x) % H;
     const int N = a.num_seqs;
     const Layout LY = layout(a.num_tokens, N, H);
-    const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
-    if (c >= cs[N] || c >= nrec) {
-        return;
-    }
-    int lo = 0, hi = N - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (cs[mid] <= c) {
-            lo = mid;
-        } else {
-            hi = mid - 1;
-        }
-    }
-    const int n = lo;
-    const int jc = c - cs[n];
+    int n = 0;
+    int jc = c;
     int bos, eos;
-    seq_bounds(a, n, bos, eos);
+    if (N == 1) {
+        // one sequence: chunk c is its c-th (no chunk-index pass ran)
+        seq_bounds(a, 0, bos, eos);
+        if (c >= (eos - bos + BT - 1) / BT || c >= nrec) {
+            return;
+        }
+    } else {
+        const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
+        if (c >= cs[N] || c >= nrec) {
+            return;
+        }
+        int lo = 0, hi = N - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (cs[mid] <= c) {
+                lo = mid;
+            } else {
+                hi = mid - 1;
+            }
+        }
+        n = lo;
+        jc = c - cs[n];
+        seq_bounds(a, n, bos, eos);
+    }
     const int t0 = bos + BT * jc;
     const int len = eos - t0 < BT ? eos - t0 : BT;
 
@@ -989,8 +999,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
     int bos, eos;
     seq_bounds(a, n, bos, eos);
-    const int c0 = cs[n];
-    const int nch = cs[n + 1] - c0;
+    // one sequence: its records start at 0 (no chunk-index pass ran)
+    const int c0 = N == 1 ? 0 : cs[n];
+    const int nch = N == 1 ? (eos - bos + BT - 1) / BT : cs[n + 1] - c0;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1502,7 +1513,7 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     char *ws = static_cast<char *>(workspace);
     KdaChunkArgs kargs = a;
     int *cs = reinterpret_cast<int *>(ws + LY.chunk_start);
-    {
+    if (a.num_seqs > 1) {  // one sequence needs no chunk index (K1 and K2 derive it)
         void *params[] = {&kargs, &cs};
         if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_index_kernel), dim3(1), dim3(1024),
                             params, 0, st) != hipSuccess) {
