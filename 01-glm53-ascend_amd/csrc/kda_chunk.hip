@@ -1501,7 +1501,7 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
         return KDA_ERR_UNSUPPORTED;
     }
     if (!aligned(a.state, 16) || (a.state_stride_slot & 3) || (a.state_stride_head & 3) ||
-        !aligned(a.q, 8) || !aligned(a.k, 8) || !aligned(a.v, 8) ||
+        !aligned(a.q, 8) || !aligned(a.k, 8) || !aligned(a.v, 8) || !aligned(a.out, 8) ||
         !aligned(a.gate, a.gate_mode == KDA_GATE_RAW ? 8 : 16)) {
         return KDA_ERR_INVALID_ARGUMENT;
     }

@@ -173,8 +173,10 @@ size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
                                  int32_t num_heads, int32_t head_dim);
 
 /* Chunked (chunk = 64 tokens) KDA over packed varlen sequences. `workspace`
- * must hold kda_chunk_workspace_bytes(...) bytes of device memory; its
- * contents need no initialization. */
+ * must hold kda_chunk_workspace_bytes(...) bytes of device memory, 256-byte
+ * aligned; its contents need no initialization. Alignment
+ * (KDA_ERR_INVALID_ARGUMENT otherwise): state 16 bytes with strides in
+ * multiples of 4 elements; q, k, v and out 8 bytes; gate 8 (RAW) or 16. */
 int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,
                      size_t workspace_bytes, void *stream);
 

@@ -57,3 +57,49 @@ def test_argument_checks_return_before_any_device_call(lib):
     lib.kda_chunk_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
                                      ctypes.c_void_p]
     assert lib.kda_chunk_launch(None, None, 0, None) != 0
+
+
+class _ChunkArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p), ("beta", ctypes.c_void_p),
+        ("A_log", ctypes.c_void_p), ("dt_bias", ctypes.c_void_p),
+        ("state", ctypes.c_void_p), ("state_stride_slot", ctypes.c_int64),
+        ("state_stride_head", ctypes.c_int64), ("num_slots", ctypes.c_int64),
+        ("state_indices", ctypes.c_void_p), ("cu_seqlens", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("track_indices", ctypes.c_void_p), ("track_lens", ctypes.c_void_p),
+        ("scale", ctypes.c_float), ("lower_bound", ctypes.c_float),
+        ("num_seqs", ctypes.c_int32), ("num_tokens", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("qk_dtype", ctypes.c_int32), ("v_dtype", ctypes.c_int32),
+        ("gate_mode", ctypes.c_int32), ("qk_l2norm", ctypes.c_int32),
+    ]
+
+
+def test_chunk_launch_alignment_checks_need_no_device(lib):
+    """The chunk launcher rejects misaligned pointers before touching the
+    device (the addresses below are never dereferenced)."""
+    lib.kda_chunk_launch.restype = ctypes.c_int
+    lib.kda_chunk_launch.argtypes = [ctypes.POINTER(_ChunkArgs), ctypes.c_void_p,
+                                     ctypes.c_size_t, ctypes.c_void_p]
+    base = 1 << 20
+
+    def args(**over):
+        a = _ChunkArgs(q=base, k=base, v=base, gate=base, beta=base, state=base,
+                       state_stride_slot=32 * 128 * 128, state_stride_head=128 * 128,
+                       num_slots=4, state_indices=base, cu_seqlens=base, out=base, scale=1.0,
+                       num_seqs=1, num_tokens=64, num_heads=32, head_dim=128, qk_dtype=0,
+                       v_dtype=0, gate_mode=1)
+        for k_, v_ in over.items():
+            setattr(a, k_, v_)
+        return a
+
+    for field, bad in (("out", base + 2), ("v", base + 2), ("q", base + 4), ("gate", base + 8),
+                       ("state", base + 8)):
+        a = args(**{field: bad})
+        assert lib.kda_chunk_launch(ctypes.byref(a), None, 0, None) == 1, field
+    a = args(state_stride_head=128 * 128 + 2)
+    assert lib.kda_chunk_launch(ctypes.byref(a), None, 0, None) == 1
+    # aligned arguments pass these checks and stop at the missing workspace
+    assert lib.kda_chunk_launch(ctypes.byref(args()), None, 0, None) == 4  # KDA_ERR_WORKSPACE
