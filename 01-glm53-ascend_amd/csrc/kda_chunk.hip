@@ -28,11 +28,14 @@
 //                           output waves compute o one phase behind; S and
 //                           vnew are exchanged through LDS.
 //
-// MFMA: v_mfma_f32_16x16x32_bf16 with fp32 accumulation. Operands whose
-// rounding would break the tolerance contract are carried as bf16 hi + lo
-// pairs (x = hi + lo to ~2^-17) and multiplied in three passes
-// (hi*hi + hi*lo + lo*hi): u = T v (T split, v exact), Aqk, q e^G, Aqk vnew and
-// the state update; Akk, w and w S run single-pass.
+// MFMA: v_mfma_f32_16x16x32_bf16 / _f16 with fp32 accumulation. Operands
+// whose rounding would break the tolerance contract are carried as bf16 hi +
+// lo pairs (x = hi + lo to ~2^-17) and multiplied in three passes
+// (hi*hi + hi*lo + lo*hi): u = T v (T split, v exact), Aqk, Aqk vnew and the
+// state update; Akk runs single-pass. w and q e^G are stored as fp16 (11-bit
+// significands, half the bytes of a bf16 pair) with a power-of-two scale per
+// fragment, and meet S as fp16 hi + lo (scaled per 32-row slice): w S single
+// pass, (q e^G) S two passes.
 //
 // Fragment conventions (lane l, r = l % 16, g = l / 16), shared by A and B so
 // that C-layout accumulators can be fed back as B operands without moving
@@ -61,22 +64,23 @@ constexpr int DK = 128;  // K == V
 constexpr int kThreads = 256;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Workspace record of one (chunk, head), in 16-byte-per-lane fragments
 // (a fragment is 64 lanes x 16 B = 1 KiB).
 constexpr int kFrag = 1024;
-constexpr int kOffW = 0;                          // w hi: A (mt 0..3, s 0..3)
-constexpr int kOffQgH = kOffW + 16 * kFrag;       // q e^G hi: A (mt, s)
-constexpr int kOffQgL = kOffQgH + 16 * kFrag;     // q e^G lo
-constexpr int kOffAqH = kOffQgL + 16 * kFrag;     // Aqk hi: A (mt, s), see aq_frag
+constexpr int kOffW = 0;                          // w fp16: A (mt 0..3, s 0..3)
+constexpr int kOffQg = kOffW + 16 * kFrag;        // q e^G fp16: A (mt, s)
+constexpr int kOffAqH = kOffQg + 16 * kFrag;      // Aqk hi: A (mt, s), see aq_frag
 constexpr int kOffAqL = kOffAqH + 6 * kFrag;      // Aqk lo
 constexpr int kOffKdH = kOffAqL + 6 * kFrag;      // kd^T hi: A (mk 0..7, s 0..1)
 constexpr int kOffKdL = kOffKdH + 16 * kFrag;     // kd^T lo
 constexpr int kOffU = kOffKdL + 16 * kFrag;       // u fp32: C (mt 0..3, vt 0..7)
 constexpr int kOffGl = kOffU + 32 * kFrag;        // e^(G_last) fp32 [128]
-constexpr int kRecBytes = kOffGl + DK * 4;        // 127488
+constexpr int kOffSc = kOffGl + DK * 4;           // fp32 [32]: 2^-shift of w (mt*4+s), q e^G (16+mt*4+s)
+constexpr int kRecBytes = kOffSc + 256;           // 111360
 // Track record of one (sequence, head): operands of the state after r < len
 // tokens of the chunk holding the tracked position.
 constexpr int kTrOffKdH = 0;
@@ -144,6 +148,71 @@ __device__ __forceinline__ void split_bf16x8(const float x[8], bf16x8 &hi, bf16x
     }
     hi = as_bf16x8(h);
     lo = as_bf16x8(l);
+}
+
+// fp16 fragments carry x * 2^sh, with sh chosen per fragment (or per S
+// slice) from its largest magnitude m so that m * 2^sh lies in [2^13, 2^14):
+// well inside fp16's range, full 11-bit significands down to 2^-27 m.
+__device__ __forceinline__ int f16_shift(float m) {
+    if (!(m > 0.f)) {
+        return 0;
+    }
+    int e;
+    (void)frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+    const int sh = 14 - e;
+    return sh < -120 ? -120 : (sh > 120 ? 120 : sh);
+}
+__device__ __forceinline__ f16x8 to_f16x8(const float x[8], int sh) {
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        h[e] = static_cast<_Float16>(ldexpf(x[e], sh));
+    }
+    return h;
+}
+// x * 2^sh = hi + lo to about 2^-22 relative (fp16, round to nearest even)
+__device__ __forceinline__ void split_f16x8(const float x[8], int sh, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float xs = ldexpf(x[e], sh);
+        const _Float16 h = static_cast<_Float16>(xs);
+        hi[e] = h;
+        lo[e] = static_cast<_Float16>(xs - static_cast<float>(h));
+    }
+}
+__device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+__device__ __forceinline__ u32x4 as_u32x4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
+
+__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Largest x over the wave, in every lane.
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp_mov<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp_mov<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp_mov<kDppRowHalfMirror>(x));
+    x = fmaxf(x, dpp_mov<kDppRowMirror>(x));
+    const float a = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)),
+                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16)));
+    const float b = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32)),
+                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48)));
+    return fmaxf(a, b);
+}
+
+// One wave stores a whole fp16 fragment and its inverse scale.
+__device__ __forceinline__ void store_frag_f16(char *rec, int off, int idx, int sc_idx, int lane,
+                                               const float x[8]) {
+    float m = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        m = fmaxf(m, fabsf(x[e]));
+    }
+    const int sh = f16_shift(wave_max(m));
+    reinterpret_cast<u32x4 *>(rec + off)[idx * 64 + lane] = as_u32x4(to_f16x8(x, sh));
+    if (lane == 0) {
+        reinterpret_cast<float *>(rec + kOffSc)[sc_idx] = ldexpf(1.f, -sh);
+    }
 }
 
 __device__ __forceinline__ void store_frag(char *base, int off, int idx, int lane, bf16x8 v) {
@@ -577,10 +646,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             }
             Rh[sl] = to_bf16x8(rv);
             split_bf16x8(qa, Qh[sl], Ql[sl]);
-            bf16x8 fh, fl;
-            split_bf16x8(qg, fh, fl);
-            store_frag(rec, kOffQgH, I * 4 + s, lane, fh);
-            store_frag(rec, kOffQgL, I * 4 + s, lane, fl);
+            store_frag_f16(rec, kOffQg, I * 4 + s, 16 + I * 4 + s, lane, qg);
         }
         // pairs (I, J), J <= I, over this half's channels
 #pragma unroll
@@ -943,7 +1009,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                     x[4 * half + i] = acc[i];
                 }
             }
-            store_frag(rec, kOffW, wave * 4 + sp, lane, to_bf16x8(x));
+            store_frag_f16(rec, kOffW, wave * 4 + sp, wave * 4 + sp, lane, x);
         }
     }
 }
@@ -976,7 +1042,8 @@ template <int NT>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws) {
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
-    __shared__ u32x4 sbuf[2][4][2][NT][64];         // S_j as B fragments: [parity][slice][hi, lo][tile][lane]
+    __shared__ u32x4 sbuf[2][4][2][NT][64];         // S_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
+    __shared__ float sscale[2][4];                  // 2^-shift of each S_j slice in sbuf
     __shared__ uint32_t vbuf[2][2][2][NT][64][4];   // vnew_j as B fragments: [parity][slice][hi, lo][tile]
     __shared__ uint32_t otile[4][16][CW / 2];       // per output wave: 16 rows x CW bf16 columns
 
@@ -1074,15 +1141,18 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // One chunk's chain operands; two sets alternate so the next chunk's
         // fragments are in flight while this chunk computes.
         struct Ops {
-            bf16x8 Wf[4], Kh[2][2], Kl[2][2];
+            f16x8 Wf[4];
+            bf16x8 Kh[2][2], Kl[2][2];
             f32x4 u[NT], gl[2];
+            float4 wsc;
         };
         auto load_ops = [&](Ops &op, int j) {
             const char *rec = rec_of(j);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                op.Wf[s] = load_frag(rec, kOffW, wr * 4 + s, lane);
+                op.Wf[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffW)[(wr * 4 + s) * 64 + lane]);
             }
+            op.wsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 16 * wr);
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -1105,37 +1175,67 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         auto step = [&](const Ops &op, int j) {
             const int p = j & 1;
             const int len = eos - (bos + BT * j) < BT ? eos - (bos + BT * j) : BT;
-            // A. publish S_j (slice wr) as hi/lo B fragments
+            // A. publish S_j (slice wr) as fp16 hi/lo B fragments, scaled by
+            // a power of two from the slice's largest magnitude
+            {
+                float m = 0.f;
 #pragma unroll
-            for (int ct = 0; ct < NT; ++ct) {
-                float x[8];
+                for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    x[i] = S[0][ct][i];
-                    x[4 + i] = S[1][ct][i];
+                    for (int ct = 0; ct < NT; ++ct) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            m = fmaxf(m, fabsf(S[tt][ct][i]));
+                        }
+                    }
                 }
-                bf16x8 hi, lo;
-                split_bf16x8(x, hi, lo);
-                sbuf[p][wr][0][ct][lane] = as_u32x4(hi);
-                sbuf[p][wr][1][ct][lane] = as_u32x4(lo);
+                const int ssh = f16_shift(wave_max(m));
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    float x[8];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        x[i] = S[0][ct][i];
+                        x[4 + i] = S[1][ct][i];
+                    }
+                    f16x8 hi, lo;
+                    split_f16x8(x, ssh, hi, lo);
+                    sbuf[p][wr][0][ct][lane] = as_u32x4(hi);
+                    sbuf[p][wr][1][ct][lane] = as_u32x4(lo);
+                }
+                if (lane == 0) {
+                    sscale[p][wr] = ldexpf(1.f, -ssh);
+                }
             }
             lds_barrier();  // B1(j)
-            // B. vnew rows [16wr, 16wr+16) = u - w S_j (single pass), published hi/lo;
+            // B. vnew rows [16wr, 16wr+16) = u - w S_j (single pass, one
+            // product per slice, then scaled), published as bf16 hi/lo;
             // tile mt = wr is half wr%2 of slice wr/2
             const int sl = wr >> 1;
             const int hf = (wr & 1) * 2;
+            float fw[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                fw[s] = op.wsc[s] * sscale[p][s];
+            }
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                f32x4 acc = z4;
+                f32x4 acc[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    acc = mfma(op.Wf[s], as_bf16x8(sbuf[p][s][0][ct][lane]), acc);
+                    acc[s] = mfma(op.Wf[s], as_f16x8(sbuf[p][s][0][ct][lane]), z4);
                 }
                 uint32_t hp[2], lp[2];
 #pragma unroll
                 for (int q2 = 0; q2 < 2; ++q2) {
-                    const float v0 = op.u[ct][2 * q2] - acc[2 * q2];
-                    const float v1 = op.u[ct][2 * q2 + 1] - acc[2 * q2 + 1];
+                    float ws0 = 0.f, ws1 = 0.f;
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        ws0 += fw[s] * acc[s][2 * q2];
+                        ws1 += fw[s] * acc[s][2 * q2 + 1];
+                    }
+                    const float v0 = op.u[ct][2 * q2] - ws0;
+                    const float v1 = op.u[ct][2 * q2 + 1] - ws1;
                     hp[q2] = pack_bf16x2(v0, v1);
                     lp[q2] = pack_bf16x2(v0 - __uint_as_float(hp[q2] << 16),
                                          v1 - __uint_as_float(hp[q2] & 0xffff0000u));
@@ -1241,15 +1341,17 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     } else {
         // ------------------------------- output waves ------------------------------
         struct OpsO {
-            bf16x8 Qh[4], Ql[4], Ah[2], Al[2];
+            f16x8 Qg[4];
+            bf16x8 Ah[2], Al[2];
+            float4 qsc;
         };
         auto load_out = [&](OpsO &op, int j) {
             const char *rec = rec_of(j);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                op.Qh[s] = load_frag(rec, kOffQgH, wr * 4 + s, lane);
-                op.Ql[s] = load_frag(rec, kOffQgL, wr * 4 + s, lane);
+                op.Qg[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffQg)[(wr * 4 + s) * 64 + lane]);
             }
+            op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 64 + 16 * wr);
             // rows [16wr, 16wr+16) meet columns >= 32 only for wr >= 2
             op.Ah[0] = load_frag(rec, kOffAqH, aq_frag(wr, 0), lane);
             op.Al[0] = load_frag(rec, kOffAqL, aq_frag(wr, 0), lane);
@@ -1315,21 +1417,32 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         };
-        // P = (q e^G) S_j (3-pass), rows [16wr, 16wr+16)
+        // P = (q e^G) S_j (fp16 q e^G against S_j hi + lo, one product per
+        // slice, then scaled), rows [16wr, 16wr+16)
         auto start = [&](const OpsO &op, int j) {
             const int p = j & 1;
+            float fq[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                fq[s] = op.qsc[s] * sscale[p][s];
+            }
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                f32x4 acc = z4;
+                f32x4 acc[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    const bf16x8 sh = as_bf16x8(sbuf[p][s][0][ct][lane]);
-                    const bf16x8 sl = as_bf16x8(sbuf[p][s][1][ct][lane]);
-                    acc = mfma(op.Qh[s], sh, acc);
-                    acc = mfma(op.Qh[s], sl, acc);
-                    acc = mfma(op.Ql[s], sh, acc);
+                    acc[s] = mfma(op.Qg[s], as_f16x8(sbuf[p][s][0][ct][lane]), z4);
+                    acc[s] = mfma(op.Qg[s], as_f16x8(sbuf[p][s][1][ct][lane]), acc[s]);
                 }
-                P[ct] = acc;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float x = 0.f;
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        x += fq[s] * acc[s][i];
+                    }
+                    P[ct][i] = x;
+                }
             }
         };
         // Iteration j: [B1(j)] finish chunk j-1 (operands in `other`), load
