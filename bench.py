@@ -60,12 +60,12 @@ DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
 # Same for config 5's 4-token verify launch (1024 sequences, H=16).
 VF_TRAFFIC = (565882.7 * FETCH_SCALE + 1063961.9 * WRITE_SCALE) * 1024
 # Same for the two prefill kernels (prepare K1, scan K2) on config 3.
-PF_TRAFFIC = ((168206.1 + 262299.2) * FETCH_SCALE + (509952.0 + 106901.7) * WRITE_SCALE) * 1024
+PF_TRAFFIC = ((168225.2 + 223851.4) * FETCH_SCALE + (444972.4 + 124021.7) * WRITE_SCALE) * 1024
 # MFMA counters of the same two kernels (profiles/prefill_chunk_t8192_h32_mfma.md): matrix work
 # executed per call (SQ_INSTS_VALU_MFMA_MOPS_* x 512 FLOP; the hi/lo operand splits roughly
 # double the algorithmic count) and the fraction of SIMD cycles each kernel keeps the MFMA busy.
-PF_MFMA_EXECUTED_FLOP = (39845888 + 136314880 + 1048576) * 512
-PF_MFMA_BUSY = {"prepare": 28311552 / (3724619 / 8 * 1024), "scan": 68157440 / (3543351 / 8 * 1024)}
+PF_MFMA_EXECUTED_FLOP = (39845888 + 69206016 + 50331648 + 1048576) * 512
+PF_MFMA_BUSY = {"prepare": 28311552 / (3707468 / 8 * 1024), "scan": 59768832 / (3466918 / 8 * 1024)}
 
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64

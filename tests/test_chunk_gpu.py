@@ -159,6 +159,36 @@ def test_prepared_chunk_matches_oracle_small(gpu_ops):
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
 
 
+@pytest.mark.parametrize("q_mul,v_mul,pool_mul", [
+    (1e7, 1.0, 1.0),    # outputs near 1e6: q e^G far beyond fp16's range unscaled
+    (1.0, 1e6, 1e6),    # states near 1e5, values 1e6
+    (1.0, 1e-6, 1e-6),  # states near 1e-8: below fp16's normal range unscaled
+    (1.0, 1.0, 1e4),    # the carried state dominates every output
+    (1.0, 1e4, 0.0),    # zero initial state, large values
+])
+def test_prepared_chunk_extreme_magnitudes(gpu_ops, q_mul, v_mul, pool_mul):
+    """The scan's fp16 operands (w, q e^G, the exchanged S slices) carry
+    power-of-two scales; magnitudes far outside fp16's range must leave the
+    error (relative to the largest output / state) inside the contract."""
+    import dataclasses
+
+    case = C.prepared_case(2, (200, 64, 1), slots=4, indices=[1, 3, 2], seed=41)
+    case = dataclasses.replace(case, q=(case.q.float() * q_mul).to(case.q.dtype),
+                               v=(case.v.float() * v_mul).to(case.v.dtype),
+                               pool=C.clone_pool(case.pool * pool_mul))
+    dev = _prepared_dev(case)
+    pool = C.to_dev(case.pool, DEV)
+    out = _chunk_prepared(gpu_ops, case, pool, dev)
+    ref_pool = C.clone_pool(case.pool).double()
+    ref = R.kda_chunk(case.q.double() * case.scale, case.k.double(), case.v.double(),
+                      case.g.double(), case.beta.double(), state_pool=ref_pool,
+                      state_indices=case.indices, cu_seqlens=case.cu_seqlens,
+                      dtype=torch.float64, out_dtype=torch.float64)
+    assert torch.isfinite(out).all() and torch.isfinite(pool).all()
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, "output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
+
+
 def test_prepared_chunk_many_sequences(gpu_ops):
     """More sequences than the chunk-index kernel has threads (1500 > 1024, so
     each thread sums several sequences' chunk counts): short ragged and empty
