@@ -1028,9 +1028,13 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 // B2(j) after vnew_j is published. S_j and vnew_j live in LDS buffers indexed
 // by j's parity. Output waves compute (q e^G) S_j between B2(j) and B1(j+1)
 // (while the chain runs its state update) and add Aqk vnew_j between B1(j+1)
-// and B2(j+1); buffer j&1 is rewritten only at chunk j+2, after both.
+// and B2(j+1); buffer j&1 is rewritten only at chunk j+2, after both. With
+// NT = 1 the chain waves compute Aqk vnew_j themselves after their state
+// update (chain wave c for rows [16c, 16c+16)) and hand it over in LDS, so
+// the output waves stream only q e^G; one extra barrier after the last chunk
+// covers the last hand-over.
 //
-// The chunk operands (w, kd, q e^G, Aqk: ~96 KiB per chunk) are the same for
+// The chunk operands (w, kd, q e^G, Aqk: ~80 KiB per chunk) are the same for
 // every column group of a (sequence, head), so a wider group (NT = 2) reads
 // fewer operand bytes per unit of work; a narrower one (NT = 1) has the
 // shorter serial step. The host picks NT from the number of chains.
@@ -1044,6 +1048,11 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     constexpr int CW = 16 * NT;
     __shared__ u32x4 sbuf[2][4][2][NT][64];         // S_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
     __shared__ float sscale[2][4];                  // 2^-shift of each S_j slice in sbuf
+    // Aqk vnew_j rows [16c, 16c+16) from chain wave c (NT = 1: the chain
+    // waves take that product so the output waves' operand stream is only
+    // q e^G)
+    constexpr bool kAqChain = NT == 1;
+    __shared__ f32x4 obuf[2][4][kAqChain ? NT : 1][64];
     __shared__ uint32_t vbuf[2][2][2][NT][64][4];   // vnew_j as B fragments: [parity][slice][hi, lo][tile]
     __shared__ uint32_t otile[4][16][CW / 2];       // per output wave: 16 rows x CW bf16 columns
 
@@ -1143,6 +1152,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         struct Ops {
             f16x8 Wf[4];
             bf16x8 Kh[2][2], Kl[2][2];
+            bf16x8 Ah[2], Al[2];  // Aqk rows [16wr, 16wr+16) (kAqChain)
             f32x4 u[NT], gl[2];
             float4 wsc;
         };
@@ -1153,6 +1163,15 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 op.Wf[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffW)[(wr * 4 + s) * 64 + lane]);
             }
             op.wsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 16 * wr);
+            if constexpr (kAqChain) {
+                // rows [16wr, 16wr+16) meet columns >= 32 only for wr >= 2
+                op.Ah[0] = load_frag(rec, kOffAqH, aq_frag(wr, 0), lane);
+                op.Al[0] = load_frag(rec, kOffAqL, aq_frag(wr, 0), lane);
+                if (wr >= 2) {
+                    op.Ah[1] = load_frag(rec, kOffAqH, aq_frag(wr, 1), lane);
+                    op.Al[1] = load_frag(rec, kOffAqL, aq_frag(wr, 1), lane);
+                }
+            }
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -1315,6 +1334,25 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                     }
                 }
             }
+            if constexpr (kAqChain) {
+                // Aqk vnew_j rows [16wr, 16wr+16) (3-pass), for output wave wr
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    f32x4 acc = z4;
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        if (s == 1 && wr < 2) {
+                            break;  // Aqk is zero there (uniform per wave)
+                        }
+                        const bf16x8 vh = vfrag(s, 0, ct);
+                        const bf16x8 vl = vfrag(s, 1, ct);
+                        acc = mfma(op.Ah[s], vh, acc);
+                        acc = mfma(op.Ah[s], vl, acc);
+                        acc = mfma(op.Al[s], vh, acc);
+                    }
+                    obuf[p][wr][ct][lane] = acc;
+                }
+            }
             if (track_slot > 0 && rr == len) {
                 store_S(track_slot, S);
             }
@@ -1335,6 +1373,11 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             load_ops(opA, j + 2 < nch ? j + 2 : nch - 1);
             step(opB, j + 1);
         }
+        if constexpr (kAqChain) {
+            if (nch > 0) {
+                lds_barrier();  // B1(nch), matched by the output waves' last finish
+            }
+        }
         if (slot > 0) {
             store_S(slot, S);
         }
@@ -1352,12 +1395,14 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 op.Qg[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffQg)[(wr * 4 + s) * 64 + lane]);
             }
             op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 64 + 16 * wr);
-            // rows [16wr, 16wr+16) meet columns >= 32 only for wr >= 2
-            op.Ah[0] = load_frag(rec, kOffAqH, aq_frag(wr, 0), lane);
-            op.Al[0] = load_frag(rec, kOffAqL, aq_frag(wr, 0), lane);
-            if (wr >= 2) {
-                op.Ah[1] = load_frag(rec, kOffAqH, aq_frag(wr, 1), lane);
-                op.Al[1] = load_frag(rec, kOffAqL, aq_frag(wr, 1), lane);
+            if constexpr (!kAqChain) {
+                // rows [16wr, 16wr+16) meet columns >= 32 only for wr >= 2
+                op.Ah[0] = load_frag(rec, kOffAqH, aq_frag(wr, 0), lane);
+                op.Al[0] = load_frag(rec, kOffAqL, aq_frag(wr, 0), lane);
+                if (wr >= 2) {
+                    op.Ah[1] = load_frag(rec, kOffAqH, aq_frag(wr, 1), lane);
+                    op.Al[1] = load_frag(rec, kOffAqL, aq_frag(wr, 1), lane);
+                }
             }
         };
         f32x4 P[NT];  // (q e^G) S of the chunk whose output is pending
@@ -1374,16 +1419,20 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
                 f32x4 acc = P[ct];
+                if constexpr (kAqChain) {
+                    acc += obuf[p][wr][ct][lane];
+                } else {
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    if (s == 1 && wr < 2) {
-                        break;  // Aqk is zero there (uniform per wave)
+                    for (int s = 0; s < 2; ++s) {
+                        if (s == 1 && wr < 2) {
+                            break;  // Aqk is zero there (uniform per wave)
+                        }
+                        const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][ct][lane][0]));
+                        const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][ct][lane][0]));
+                        acc = mfma(op.Ah[s], vh, acc);
+                        acc = mfma(op.Ah[s], vl, acc);
+                        acc = mfma(op.Al[s], vh, acc);
                     }
-                    const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][ct][lane][0]));
-                    const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][ct][lane][0]));
-                    acc = mfma(op.Ah[s], vh, acc);
-                    acc = mfma(op.Ah[s], vl, acc);
-                    acc = mfma(op.Al[s], vh, acc);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -1456,6 +1505,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             lds_barrier();  // B2(j)
             start(cur, j);
             if (j == nch - 1) {
+                if constexpr (kAqChain) {
+                    lds_barrier();  // B1(nch): the chain's last Aqk vnew is in obuf
+                }
                 finish(cur, j);
             }
         };
