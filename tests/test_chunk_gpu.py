@@ -262,3 +262,53 @@ def test_chunk_no_tokens_tracks_initial_state(gpu_ops):
     assert torch.equal(got[5], torch.zeros_like(got[5])), "slot-0 request tracks a zero state"
     for s in (0, 1, 2, 3):
         assert torch.equal(got[s], case.pool[s]), f"slot {s} changed"
+
+
+def test_chunk_c_abi_launch_direct(gpu_ops):
+    """kda_chunk_launch through ctypes with a caller-owned workspace (no torch
+    operator in between): against the oracle, bitwise equal to the torch op,
+    and the same workspace reused by a second, smaller call."""
+    import ctypes
+
+    from sgl_glm53_ascend_ops._load import abi_library_path
+    from tests.test_abi_exports import _ChunkArgs
+
+    lib = ctypes.CDLL(str(abi_library_path()))
+    lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
+    lib.kda_chunk_workspace_bytes.argtypes = [ctypes.c_int32] * 4
+    lib.kda_chunk_launch.restype = ctypes.c_int
+    lib.kda_chunk_launch.argtypes = [ctypes.POINTER(_ChunkArgs), ctypes.c_void_p,
+                                     ctypes.c_size_t, ctypes.c_void_p]
+    stream = torch.cuda.current_stream().cuda_stream
+    big = C.prepared_case(3, (150, 64, 9), slots=5, indices=[4, 0, 2], seed=23)
+    T_big = int(big.cu_seqlens[-1])
+    nbytes = lib.kda_chunk_workspace_bytes(T_big, 3, 3, 128)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    for case in (big, C.prepared_case(3, (40, 70), slots=5, indices=[1, 3], seed=24)):
+        dev = _prepared_dev(case)
+        pool = C.to_dev(case.pool, DEV)
+        idx = case.indices.to(DEV)
+        cu = case.cu_seqlens.to(DEV)
+        out = torch.empty_like(dev["v"])
+        T, H, D = case.q.shape[1:]
+        a = _ChunkArgs(q=dev["q"].data_ptr(), k=dev["k"].data_ptr(), v=dev["v"].data_ptr(),
+                       gate=dev["g"].data_ptr(), beta=dev["beta"].data_ptr(),
+                       state=pool.data_ptr(), state_stride_slot=pool.stride(0),
+                       state_stride_head=pool.stride(1), num_slots=pool.shape[0],
+                       state_indices=idx.data_ptr(), cu_seqlens=cu.data_ptr(),
+                       out=out.data_ptr(), scale=case.scale, num_seqs=len(case.indices),
+                       num_tokens=T, num_heads=H, head_dim=D, qk_dtype=0, v_dtype=0,
+                       gate_mode=1, qk_l2norm=0)
+        assert lib.kda_chunk_workspace_bytes(T, len(case.indices), H, D) <= nbytes
+        assert lib.kda_chunk_launch(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()),
+                                    ctypes.c_size_t(nbytes), ctypes.c_void_p(stream)) == 0
+        torch.cuda.synchronize()
+        ref_pool = C.clone_pool(case.pool)
+        ref = R.kda_chunk(case.q.float() * case.scale, case.k, case.v, case.g, case.beta,
+                          state_pool=ref_pool, state_indices=case.indices,
+                          cu_seqlens=case.cu_seqlens, out_dtype=torch.float32)
+        C.assert_out(out.cpu(), ref, C.OUT_TOL, "output")
+        C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
+        pool_op = C.to_dev(case.pool, DEV)
+        out_op = _chunk_prepared(gpu_ops, case, pool_op, dev)
+        assert torch.equal(out, out_op) and torch.equal(pool, pool_op)
