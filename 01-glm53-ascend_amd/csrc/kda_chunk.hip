@@ -52,6 +52,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "kda_abi.h"
 #include "kda_device.h"
@@ -93,6 +94,7 @@ struct Layout {
     size_t chunk_start;  // int32 [N+1]
     size_t recs;         // kRecBytes x (max_chunks x H)
     size_t tracks;       // kTrBytes x (N x H)
+    size_t carry;        // one sequence: fp32 [H][V][K], the state between scan segments
     size_t total;
 };
 
@@ -109,9 +111,17 @@ __host__ __device__ inline Layout layout(int T, int N, int H) {
     L.chunk_start = 0;
     L.recs = align256(static_cast<size_t>(N + 1) * 4);
     L.tracks = L.recs + static_cast<size_t>(kRecBytes) * max_chunks(T, N) * H;
-    L.total = L.tracks + static_cast<size_t>(kTrBytes) * N * H;
+    L.carry = L.tracks + static_cast<size_t>(kTrBytes) * N * H;
+    L.total = L.carry + (N == 1 ? static_cast<size_t>(DK) * DK * 4 * H : 0);
     return L;
 }
+
+// A long single sequence whose scan would leave half the CUs idle is run in
+// two segments: K1 of the second segment overlaps the first segment's scan
+// on a second stream (segment 0 = the whole sequence). The first segment
+// holds this many of the sequence's nch chunks (~47%: the best of 35-62%
+// measured on config 5).
+__host__ __device__ inline int split_chunk(int nch) { return (nch * 47 + 50) / 100; }
 
 __device__ __forceinline__ int kperm(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
 
@@ -348,7 +358,7 @@ static_assert(sizeof(PrepShared) <= 54 * 1024, "the prepare kernel's LDS budget"
 
 template <int GATE>
 __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkArgs a, char *ws,
-                                                                 int nrec) {
+                                                                 int nrec, int seg) {
     __shared__ PrepShared sm;
     // Workgroups run chunk-descending, heads fastest: the scan starts with the
     // first chunk of every sequence and head, so those records are written
@@ -365,8 +375,12 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     if (N == 1) {
         // one sequence: chunk c is its c-th (no chunk-index pass ran)
         seq_bounds(a, 0, bos, eos);
-        if (c >= (eos - bos + BT - 1) / BT || c >= nrec) {
+        const int nch = (eos - bos + BT - 1) / BT;
+        if (c >= nch || c >= nrec) {
             return;
+        }
+        if (seg != 0 && (c < split_chunk(nch)) != (seg == 1)) {
+            return;  // the other segment's chunk
         }
     } else {
         const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
@@ -1043,7 +1057,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 constexpr int kScanThreads = 512;
 
 template <int NT>
-__global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws) {
+__global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws,
+                                                                  int seg) {
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
     __shared__ u32x4 sbuf[2][4][2][NT][64];         // S_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
@@ -1078,6 +1093,11 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     // one sequence: its records start at 0 (no chunk-index pass ran)
     const int c0 = N == 1 ? 0 : cs[n];
     const int nch = N == 1 ? (eos - bos + BT - 1) / BT : cs[n + 1] - c0;
+    // chunks [j0, j1) of this launch (segments 1 and 2: one sequence only)
+    const int j0 = seg == 2 ? split_chunk(nch) : 0;
+    const int j1 = seg == 1 ? split_chunk(nch) : nch;
+    float *carry = reinterpret_cast<float *>(const_cast<char *>(ws) + LY.carry) +
+                   static_cast<size_t>(h) * DK * DK;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1119,12 +1139,19 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 
         // S rows [32wr, 32wr+32): tiles (kt = 2wr + tt, ct), lane holds
         // S[16kt + 4gq + i][col0 + 16ct + r].
+        // the same element in the carry buffer between segments
+        auto carry_ptr = [&](int tt, int ct) {
+            return carry + static_cast<int64_t>(col0 + 16 * ct + r) * DK + 16 * (2 * wr + tt) + 4 * gq;
+        };
         f32x4 S[2][NT];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                if (slot > 0) {
+                if (seg == 2) {
+                    const float4 s4 = load4(carry_ptr(tt, ct));
+                    S[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
+                } else if (slot > 0) {
                     const float4 s4 = load4(state_ptr(slot, tt, ct));
                     S[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
                 } else {
@@ -1142,7 +1169,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         };
-        if (track_slot > 0 && track_len == 0) {
+        if (track_slot > 0 && track_len == 0 && seg != 2) {
             store_S(track_slot, S);
         }
         const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
@@ -1361,24 +1388,33 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // The prefetches are unconditional (clamped to the last chunk) so the
         // compiler's wait counts stay exact on every path through the loop.
         Ops opA, opB;
-        if (nch > 0) {
-            load_ops(opA, 0);
+        if (j1 > j0) {
+            load_ops(opA, j0);
         }
-        for (int j = 0; j < nch; j += 2) {
-            load_ops(opB, j + 1 < nch ? j + 1 : nch - 1);
+        for (int j = j0; j < j1; j += 2) {
+            load_ops(opB, j + 1 < j1 ? j + 1 : j1 - 1);
             step(opA, j);
-            if (j + 1 >= nch) {
+            if (j + 1 >= j1) {
                 break;
             }
-            load_ops(opA, j + 2 < nch ? j + 2 : nch - 1);
+            load_ops(opA, j + 2 < j1 ? j + 2 : j1 - 1);
             step(opB, j + 1);
         }
         if constexpr (kAqChain) {
-            if (nch > 0) {
-                lds_barrier();  // B1(nch), matched by the output waves' last finish
+            if (j1 > j0) {
+                lds_barrier();  // B1(j1), matched by the output waves' last finish
             }
         }
-        if (slot > 0) {
+        if (seg == 1) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    *reinterpret_cast<float4 *>(carry_ptr(tt, ct)) =
+                        make_float4(S[tt][ct][0], S[tt][ct][1], S[tt][ct][2], S[tt][ct][3]);
+                }
+            }
+        } else if (slot > 0) {
             store_S(slot, S);
         }
     } else {
@@ -1498,13 +1534,13 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // chunk j+1 into `other`, [B2(j)] start chunk j (operands in `cur`).
         auto iter = [&](const OpsO &cur, OpsO &other, int j) {
             lds_barrier();  // B1(j)
-            if (j > 0) {
+            if (j > j0) {
                 finish(other, j - 1);
             }
-            load_out(other, j + 1 < nch ? j + 1 : nch - 1);
+            load_out(other, j + 1 < j1 ? j + 1 : j1 - 1);
             lds_barrier();  // B2(j)
             start(cur, j);
-            if (j == nch - 1) {
+            if (j == j1 - 1) {
                 if constexpr (kAqChain) {
                     lds_barrier();  // B1(nch): the chain's last Aqk vnew is in obuf
                 }
@@ -1512,8 +1548,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
         };
         OpsO opA, opB;
-        if (nch > 0) {
-            load_out(opA, 0);
+        if (j1 > j0) {
+            load_out(opA, j0);
         }
         // L2 warm-up: at chunk j each workgroup reads one dword of each line of
         // its 1/NV share of chunk j + kWarmAhead's record (996 cache lines), so
@@ -1531,7 +1567,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             wb[k] = 0;
         }
         auto touch = [&](uint32_t (&dst)[kTouch], int jj) {
-            const char *rec = rec_of(jj < nch ? jj : nch - 1);
+            const char *rec = rec_of(jj < j1 ? jj : j1 - 1);
 #pragma unroll
             for (int k = 0; k < kTouch; ++k) {
                 warm ^= dst[k];
@@ -1542,10 +1578,10 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 dst[k] = *reinterpret_cast<const uint32_t *>(rec + l * 128);
             }
         };
-        for (int j = 0; j < nch; j += 2) {
+        for (int j = j0; j < j1; j += 2) {
             touch(wa, j + kWarmAhead);
             iter(opA, opB, j);
-            if (j + 1 >= nch) {
+            if (j + 1 >= j1) {
                 break;
             }
             touch(wb, j + 1 + kWarmAhead);
@@ -1572,10 +1608,10 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
         }
     };
-    if (n == 0) {
+    if (n == 0 && seg != 2) {
         zero_rows(0, bos);
     }
-    if (n == N - 1) {
+    if (n == N - 1 && seg != 1) {
         zero_rows(eos, a.num_tokens);
     }
 }
@@ -1620,6 +1656,55 @@ const void *scan_kernel(int nt) {
 }
 
 int64_t scan_blocks(int64_t pairs, int nt) { return (pairs + 7) / 8 * 8 * (8 / nt); }
+
+// A second stream (default priority) and two events per device, created on
+// first use and kept for the process: the split prefill forks K1 of its
+// second segment onto the stream and joins it back before the second scan.
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr;
+    hipEvent_t join = nullptr;
+};
+
+bool side_stream(hipStream_t main, SideStream &out) {
+    static std::mutex mu;
+    static SideStream streams[64];
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(main, &dev) != hipSuccess) {
+        (void)hipGetLastError();
+        if (hipGetDevice(&dev) != hipSuccess) {
+            return false;
+        }
+    }
+    if (dev < 0 || dev >= 64) {
+        return false;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    SideStream &ss = streams[dev];
+    if (ss.stream == nullptr) {
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess) {
+            return false;
+        }
+        SideStream fresh;
+        const bool ok = hipSetDevice(dev) == hipSuccess &&
+                        hipStreamCreateWithFlags(&fresh.stream, hipStreamNonBlocking) == hipSuccess &&
+                        hipEventCreateWithFlags(&fresh.fork, hipEventDisableTiming) == hipSuccess &&
+                        hipEventCreateWithFlags(&fresh.join, hipEventDisableTiming) == hipSuccess;
+        (void)hipSetDevice(cur);
+        if (!ok) {
+            (void)hipGetLastError();
+            return false;
+        }
+        ss = fresh;
+    }
+    out = ss;
+    return true;
+}
+
+// Single sequences at least this long whose scan fills at most half the CUs
+// take the two-segment path.
+constexpr int kSplitMinTokens = 8192;
 
 }  // namespace chunk
 }  // namespace kda
@@ -1686,35 +1771,45 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
         }
     }
     const int nrec = max_chunks(a.num_tokens, a.num_seqs);
-    {
-        const void *fn = a.gate_mode == KDA_GATE_RAW
-                             ? reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_RAW>)
-                             : reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_LOG>);
-        int nr = nrec;
-        void *params[] = {&kargs, &ws, &nr};
-        const int64_t prep_blocks = static_cast<int64_t>(nrec) * a.num_heads;
-        if (prep_blocks > 0x7fffffff) {
-            return KDA_ERR_INVALID_ARGUMENT;
-        }
-        if (hipLaunchKernel(fn, dim3(static_cast<unsigned>(prep_blocks)),
-                            dim3(kThreads), params, 0, st) != hipSuccess) {
-            return KDA_ERR_LAUNCH;
-        }
+    const int64_t prep_blocks = static_cast<int64_t>(nrec) * a.num_heads;
+    const int64_t pairs = static_cast<int64_t>(a.num_seqs) * a.num_heads;
+    const int nt = scan_tiles(pairs, st);
+    const int64_t blocks = scan_blocks(pairs, nt);
+    if (prep_blocks > 0x7fffffff || blocks > 0x7fffffff) {
+        return KDA_ERR_INVALID_ARGUMENT;
     }
-    {
-        const int64_t pairs = static_cast<int64_t>(a.num_seqs) * a.num_heads;
-        const int nt = scan_tiles(pairs, st);
-        const int64_t blocks = scan_blocks(pairs, nt);
-        if (blocks > 0x7fffffff) {
-            return KDA_ERR_INVALID_ARGUMENT;
-        }
+    const void *prep = a.gate_mode == KDA_GATE_RAW
+                           ? reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_RAW>)
+                           : reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_LOG>);
+    auto launch_prep = [&](int seg, hipStream_t s) {
+        int nr = nrec;
+        int sg = seg;
+        void *params[] = {&kargs, &ws, &nr, &sg};
+        return hipLaunchKernel(prep, dim3(static_cast<unsigned>(prep_blocks)), dim3(kThreads),
+                               params, 0, s) == hipSuccess;
+    };
+    auto launch_scan = [&](int seg) {
         const char *cws = ws;
-        void *params[] = {&kargs, &cws};
-        if (hipLaunchKernel(scan_kernel(nt),
-                            dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads), params, 0,
-                            st) != hipSuccess) {
-            return KDA_ERR_LAUNCH;
-        }
+        int sg = seg;
+        void *params[] = {&kargs, &cws, &sg};
+        return hipLaunchKernel(scan_kernel(nt), dim3(static_cast<unsigned>(blocks)),
+                               dim3(kScanThreads), params, 0, st) == hipSuccess;
+    };
+    SideStream side;
+    const bool split = a.num_seqs == 1 && nt == 1 && a.num_tokens >= kSplitMinTokens &&
+                       pairs * 8 * 2 <= device_cus(st) && side_stream(st, side);
+    if (!split) {
+        return launch_prep(0, st) && launch_scan(0) ? KDA_OK : KDA_ERR_LAUNCH;
+    }
+    // st:    K1(seg 1) -> fork -> K2(seg 1) -> [wait join] -> K2(seg 2)
+    // side:                [wait fork] -> K1(seg 2) -> join
+    // (the side stream starts after K1 of the first segment, so its K1 runs
+    // on the CUs the first scan leaves idle)
+    if (!launch_prep(1, st) || hipEventRecord(side.fork, st) != hipSuccess ||
+        hipStreamWaitEvent(side.stream, side.fork, 0) != hipSuccess || !launch_prep(2, side.stream) ||
+        hipEventRecord(side.join, side.stream) != hipSuccess || !launch_scan(1) ||
+        hipStreamWaitEvent(st, side.join, 0) != hipSuccess || !launch_scan(2)) {
+        return KDA_ERR_LAUNCH;
     }
     return KDA_OK;
 }

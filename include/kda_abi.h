@@ -168,13 +168,18 @@ typedef struct KdaChunkArgs {
 } KdaChunkArgs;
 
 /* Bytes of device scratch kda_chunk_launch needs for these arguments. An
- * upper bound that depends only on T, N, H and D (no device reads). */
+ * upper bound that depends only on T, N, H and D (no device reads): the
+ * chunk records, the tracking records and, when N == 1, the state carried
+ * between the two scan segments of a long sequence. */
 size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
                                  int32_t num_heads, int32_t head_dim);
 
 /* Chunked (chunk = 64 tokens) KDA over packed varlen sequences. `workspace`
  * must hold kda_chunk_workspace_bytes(...) bytes of device memory, 256-byte
- * aligned; its contents need no initialization. Alignment
+ * aligned; its contents need no initialization. A single long sequence on few
+ * heads forks its second segment's preparation onto a library-owned stream
+ * and joins it back on `stream` (event fork/join; graph-capture safe).
+ * Alignment
  * (KDA_ERR_INVALID_ARGUMENT otherwise): state 16 bytes with strides in
  * multiples of 4 elements; q, k, v and out 8 bytes; gate 8 (RAW) or 16. */
 int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,

@@ -145,3 +145,44 @@ def test_prefill_tracking_graph_replay(gpu_ops, op):
         assert torch.equal(captured.cpu(), expected), f"replay {replay}: output"
         assert torch.equal(work.cpu(), ref_pool), f"replay {replay}: pool"
         assert expected.float().abs().sum() > 0
+
+
+def test_chunk_two_segment_graph_replay(gpu_ops):
+    """One long sequence on few heads takes the chunk op's two-segment path
+    (a second stream forked and joined inside the op): captured once, replayed
+    with the slot (padding slot 0 included), the sequence bounds and the
+    tracked length moved across the segment boundary."""
+    T = 8192
+    initial = C.to_dev(C.native_pool(6, H, D, seed=70), DEV)
+    work, reference = C.clone_pool(initial), C.clone_pool(initial)
+    inp = _Inputs(T, seed=71)
+    slots = torch.tensor([1], dtype=torch.int32, device=DEV)
+    dests = torch.tensor([4], dtype=torch.int32, device=DEV)
+    cuts = torch.tensor([100], dtype=torch.int32, device=DEV)
+    starts = _offsets([T])
+
+    def run(pool):
+        return gpu_ops.kda_varlen_chunk(**inp.const, **inp.t, initial_state_source=pool,
+                                        initial_state_indices=slots, cu_seqlens=starts,
+                                        prefill=True, track_state_indices=dests,
+                                        track_state_lens=cuts)
+
+    graph, captured = _capture(lambda: run(work))
+    bounds = [(0, T), (37, 8150), (0, T), (5, 4000)]
+    for replay in range(8):
+        lo, hi = bounds[replay % len(bounds)]
+        slots.copy_(torch.tensor([replay % 3], dtype=torch.int32))
+        cuts.copy_(torch.tensor([[0, 100, 3840, 3841, 6000, hi - lo, 64, 129][replay]],
+                                dtype=torch.int32))
+        starts.copy_(torch.tensor([lo, hi], dtype=torch.int32))
+        inp.refresh(replay)
+        work.copy_(initial)
+        reference.copy_(initial)
+        expected = run(reference)
+        torch.cuda.synchronize()
+        expected, ref_pool = expected.cpu(), reference.cpu()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured.cpu(), expected), f"replay {replay}: output"
+        assert torch.equal(work.cpu(), ref_pool), f"replay {replay}: pool"
+        assert expected.float().abs().sum() > 0
