@@ -1056,9 +1056,12 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 
 constexpr int kScanThreads = 512;
 
-template <int NT>
+// SEG: the two-segment form (seg_arg 1 or 2); without it every launch scans
+// the whole sequence and the segment logic compiles away.
+template <int NT, bool SEG>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws,
-                                                                  int seg) {
+                                                                  int seg_arg) {
+    const int seg = SEG ? seg_arg : 0;
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
     __shared__ u32x4 sbuf[2][4][2][NT][64];         // S_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
@@ -1650,9 +1653,10 @@ int device_cus(hipStream_t stream) {
 // µs for the scan).
 int scan_tiles(int64_t pairs, hipStream_t stream) { return pairs * 8 <= device_cus(stream) ? 1 : 2; }
 
-const void *scan_kernel(int nt) {
-    return nt == 2 ? reinterpret_cast<const void *>(chunk_scan_kernel<2>)
-                   : reinterpret_cast<const void *>(chunk_scan_kernel<1>);
+const void *scan_kernel(int nt, bool seg) {
+    return nt == 2 ? reinterpret_cast<const void *>(chunk_scan_kernel<2, false>)
+           : seg   ? reinterpret_cast<const void *>(chunk_scan_kernel<1, true>)
+                   : reinterpret_cast<const void *>(chunk_scan_kernel<1, false>);
 }
 
 int64_t scan_blocks(int64_t pairs, int nt) { return (pairs + 7) / 8 * 8 * (8 / nt); }
@@ -1792,7 +1796,7 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
         const char *cws = ws;
         int sg = seg;
         void *params[] = {&kargs, &cws, &sg};
-        return hipLaunchKernel(scan_kernel(nt), dim3(static_cast<unsigned>(blocks)),
+        return hipLaunchKernel(scan_kernel(nt, seg != 0), dim3(static_cast<unsigned>(blocks)),
                                dim3(kScanThreads), params, 0, st) == hipSuccess;
     };
     SideStream side;
