@@ -1664,14 +1664,18 @@ int64_t scan_blocks(int64_t pairs, int nt) { return (pairs + 7) / 8 * 8 * (8 / n
 // A second stream (default priority) and two events per device, created on
 // first use and kept for the process: the split prefill forks K1 of its
 // second segment onto the stream and joins it back before the second scan.
+// `order` is held across one call's fork / join sequence, so calls from
+// several host threads cannot interleave their event records and waits.
 struct SideStream {
     hipStream_t stream = nullptr;
     hipEvent_t fork = nullptr;
     hipEvent_t join = nullptr;
+    std::mutex *order = nullptr;
 };
 
 bool side_stream(hipStream_t main, SideStream &out) {
     static std::mutex mu;
+    static std::mutex orders[64];
     static SideStream streams[64];
     hipDevice_t dev = 0;
     if (hipStreamGetDevice(main, &dev) != hipSuccess) {
@@ -1700,6 +1704,7 @@ bool side_stream(hipStream_t main, SideStream &out) {
             (void)hipGetLastError();
             return false;
         }
+        fresh.order = &orders[dev];
         ss = fresh;
     }
     out = ss;
@@ -1809,6 +1814,7 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     // side:                [wait fork] -> K1(seg 2) -> join
     // (the side stream starts after K1 of the first segment, so its K1 runs
     // on the CUs the first scan leaves idle)
+    std::lock_guard<std::mutex> lock(*side.order);
     if (!launch_prep(1, st) || hipEventRecord(side.fork, st) != hipSuccess ||
         hipStreamWaitEvent(side.stream, side.fork, 0) != hipSuccess || !launch_prep(2, side.stream) ||
         hipEventRecord(side.join, side.stream) != hipSuccess || !launch_scan(1) ||
