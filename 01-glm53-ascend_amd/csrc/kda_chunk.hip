@@ -1712,8 +1712,10 @@ bool side_stream(hipStream_t main, SideStream &out) {
 }
 
 // Single sequences at least this long whose scan fills at most half the CUs
-// take the two-segment path.
-constexpr int kSplitMinTokens = 8192;
+// take the two-segment path (measured: T = 8192 loses 8-9 µs to the extra
+// launches and the fork / join, T = 16384 on 8 heads gains 13 µs, config 5's
+// 65536 tokens on 16 heads 200 µs).
+constexpr int kSplitMinTokens = 16384;
 
 }  // namespace chunk
 }  // namespace kda

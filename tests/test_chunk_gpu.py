@@ -314,29 +314,30 @@ def test_chunk_c_abi_launch_direct(gpu_ops):
         assert torch.equal(out, out_op) and torch.equal(pool, pool_op)
 
 
-# A single sequence of at least 8192 tokens whose scan leaves half the CUs idle
-# (heads x 16 <= CUs) runs in two segments, the first ~47% of its chunks and
-# the rest, with the second segment's prepare kernel on a second stream; the
-# state between them goes through the workspace. 128 chunks split at 60.
-_SPLIT = 60 * 64
+# A single sequence of at least 16384 tokens whose scan leaves half the CUs
+# idle (heads x 16 <= CUs) runs in two segments, the first ~47% of its chunks
+# and the rest, with the second segment's prepare kernel on a second stream;
+# the state between them goes through the workspace. 256 chunks split at 120.
+_SPLIT = 120 * 64
+_T_SPLIT = 16384
 
 
 @pytest.mark.parametrize("label,bounds,slot,track", [
-    ("whole", (0, 8192), 1, None),
-    ("zero slot", (0, 8192), 0, None),
-    ("offset and ragged", (37, 8150), 2, None),
+    ("whole", (0, _T_SPLIT), 1, None),
+    ("zero slot", (0, _T_SPLIT), 0, None),
+    ("offset and ragged", (37, _T_SPLIT - 42), 2, None),
     ("short sequence", (5, 100), 1, None),
-    ("track at 0", (0, 8192), 1, 0),
-    ("track in first segment", (0, 8192), 1, 1000),
-    ("track at split", (0, 8192), 1, _SPLIT),
-    ("track after split", (0, 8192), 1, _SPLIT + 1),
-    ("track in second segment", (0, 8192), 0, 7000),
-    ("track at end", (0, 8192), 1, 8192),
+    ("track at 0", (0, _T_SPLIT), 1, 0),
+    ("track in first segment", (0, _T_SPLIT), 1, 1000),
+    ("track at split", (0, _T_SPLIT), 1, _SPLIT),
+    ("track after split", (0, _T_SPLIT), 1, _SPLIT + 1),
+    ("track in second segment", (0, _T_SPLIT), 0, 14000),
+    ("track at end", (0, _T_SPLIT), 1, _T_SPLIT),
 ])
 def test_chunk_two_segment_path(gpu_ops, label, bounds, slot, track):
     import dataclasses
 
-    case = C.raw_case(2, (8192,), indices=[slot], slots=4, seed=777 + len(label),
+    case = C.raw_case(1, (_T_SPLIT,), indices=[slot], slots=4, seed=777 + len(label),
                       track=None if track is None else ([3], [track]))
     case = dataclasses.replace(case, cu_seqlens=torch.tensor(bounds, dtype=torch.int32))
     out, pool = _run_chunk(gpu_ops, case)

@@ -152,7 +152,7 @@ def test_chunk_two_segment_graph_replay(gpu_ops):
     (a second stream forked and joined inside the op): captured once, replayed
     with the slot (padding slot 0 included), the sequence bounds and the
     tracked length moved across the segment boundary."""
-    T = 8192
+    T = 16384
     initial = C.to_dev(C.native_pool(6, H, D, seed=70), DEV)
     work, reference = C.clone_pool(initial), C.clone_pool(initial)
     inp = _Inputs(T, seed=71)
@@ -168,11 +168,11 @@ def test_chunk_two_segment_graph_replay(gpu_ops):
                                         track_state_lens=cuts)
 
     graph, captured = _capture(lambda: run(work))
-    bounds = [(0, T), (37, 8150), (0, T), (5, 4000)]
+    bounds = [(0, T), (37, T - 42), (0, T), (5, 4000)]
     for replay in range(8):
         lo, hi = bounds[replay % len(bounds)]
         slots.copy_(torch.tensor([replay % 3], dtype=torch.int32))
-        cuts.copy_(torch.tensor([[0, 100, 3840, 3841, 6000, hi - lo, 64, 129][replay]],
+        cuts.copy_(torch.tensor([[0, 100, 7680, 7681, 12000, hi - lo, 64, 129][replay]],
                                 dtype=torch.int32))
         starts.copy_(torch.tensor([lo, hi], dtype=torch.int32))
         inp.refresh(replay)
