@@ -481,7 +481,10 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
 
     // Tokens no sequence covers are zero (the reference allocates
     // zeros_like(v), kda_varlen_recurrent.cpp:142): the first request zeroes
-    // [0, cu[0]) and the last one [cu[N], T).
+    // [0, cu[0]) and the last one [cu[N], T). The DECAY form writes a
+    // caller-owned output and touches only the rows its requests cover, as
+    // the reference's prepared kernels do (prepared_recurrent.cpp:386-560),
+    // so a caller may launch request by request into one buffer.
     auto zero_rows = [&](int t0, int t1) {
         float z[NP];
 #pragma unroll
@@ -492,11 +495,13 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
             store_row<TV, NP, RS>(op + (static_cast<int64_t>(t) * H + head) * D + row0, z, kc);
         }
     };
-    if (n == 0) {
-        zero_rows(0, bos);
-    }
-    if (n == a.num_seqs - 1) {
-        zero_rows(eos, T);
+    if constexpr (GATE != KDA_GATE_DECAY) {
+        if (n == 0) {
+            zero_rows(0, bos);
+        }
+        if (n == a.num_seqs - 1) {
+            zero_rows(eos, T);
+        }
     }
 
     if (a.intermediate == nullptr && slot > 0) {

@@ -5,6 +5,6 @@ native operator library, which registers ``torch.ops.sgl_glm53_ascend.*``
 (reference: sgl-glm53-ascend-ops/src/sgl_glm53_ascend_ops/__init__.py:1-5).
 """
 
-from ._load import load_library
+from ._load import abi, chunk_workspace_bytes, load_library
 
 load_library()

@@ -9,6 +9,7 @@ CPU/eager implementation of these operators.
 
 from __future__ import annotations
 
+import ctypes
 from pathlib import Path
 
 import torch
@@ -47,3 +48,24 @@ def load_library() -> None:
         return
     torch.ops.load_library(str(_find_library()))
     _LOADED = True
+
+
+_ABI = None
+
+
+def abi() -> ctypes.CDLL:
+    """The C-ABI library (``include/kda_abi.h``) through ctypes, loaded once."""
+    global _ABI
+    if _ABI is None:
+        lib = ctypes.CDLL(str(abi_library_path()))
+        lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
+        lib.kda_chunk_workspace_bytes.argtypes = [ctypes.c_int32] * 4
+        _ABI = lib
+    return _ABI
+
+
+def chunk_workspace_bytes(num_tokens: int, num_seqs: int, num_heads: int,
+                          head_dim: int = 128) -> int:
+    """Device scratch the chunked prefill takes for these sizes
+    (``kda_chunk_workspace_bytes``)."""
+    return int(abi().kda_chunk_workspace_bytes(num_tokens, num_seqs, num_heads, head_dim))

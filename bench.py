@@ -9,22 +9,42 @@ permutation of 256 of the slots, updated in place. One *step* is one call of
 the decode operator over the whole batch (every step advances all 256
 sequences by one token in place). ``value`` = tokens/s = 256 / step time.
 
-Also reported (same JSON line): the chunked prefill of ``configs[2]`` (T=8192
-single sequence, H=32, K=V=128, chunk 64) as ``prefill``, the decode kernel's
-roofline (algorithmic bytes / kernel time, measured with HIP events on the
-launch stream), ``more_configs`` (configs 4 and 5 prefill and config 5's
-4-token decode, a few timed calls each, inputs drawn on the device) and the CPU
-baseline (this repository's torch oracle of the reference CPU path, on the
-host cores, over a bounded sample).
+Also reported in the same JSON line:
+
+* ``prefill`` -- the chunked prefill of ``configs[2]`` (T=8192, one sequence,
+  H=32, K=V=128, chunk 64);
+* ``roofline`` -- the decode kernel: algorithmic bytes / HIP-event time per
+  call on the launch stream; ``traffic`` is the HBM bytes per launch from the
+  committed rocprofv3 counter summary, used only while the kernel source it was
+  measured on is unchanged (``source_sha256`` in the summary);
+* ``more_configs`` -- configs 4 and 5 (prefill) and config 5's 4-token decode;
+* ``latency_rows`` -- the reference bench's deployed shapes
+  (bench/kda_recurrent/bench_kda_varlen_recurrent.py:81-114,534-551): decode
+  H16/32/64 x B1/32/128, the five checkpointed verify shapes, recurrent
+  prefill H4/H8, each validated against the oracle and timed;
+* ``cpu_baseline`` -- this repository's torch oracle of the reference CPU path
+  on the host cores over a bounded sample; the same leg is the checker that
+  validates every timed workload before it is timed (``validated``). A failed
+  validation makes the run exit non-zero.
+
+Every timed workload first runs a settle phase (batches of 10 calls until two
+successive batch means agree within 1%, at least ``--settle`` calls) so the
+figures are steady-state whatever ``--warmup`` the caller passes; the call
+count is reported as ``settle_calls``.
 
 Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-more]``.
+Profiling aids: ``--summarize-trace CSV``, ``--summarize-counters CSV``,
+``--copy-calibration MIB``.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
+import hashlib
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -38,132 +58,164 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 BF16_PEAK_TFLOPS = 2500.0  # MI355X published dense bf16 MFMA
+CSRC = os.path.join(ROOT, "01-glm53-ascend_amd", "csrc")
+PROFILES = os.path.join(ROOT, "profiles")
 
 # Config 2 (decode) shape.
 DEC_N, DEC_H, DEC_D, DEC_SLOTS = 256, 32, 128, 512
 # Algorithmic bytes per token-head: state read + write (2*D*D*4), q, k, v
 # (3*D*2), g (D*4), beta (4), o (D*2).
 BYTES_PER_TOKEN_HEAD = 2 * DEC_D * DEC_D * 4 + 3 * DEC_D * 2 + DEC_D * 4 + 4 + DEC_D * 2
-# + cu_seqlens (257 x 4) + indices (256 x 4) + ... as quoted: 2052 B of metadata.
+# + cu_seqlens (257 x 4) + indices (256 x 4): 2052 B of metadata.
 DEC_BYTES = DEC_N * DEC_H * BYTES_PER_TOKEN_HEAD + (DEC_N + 1) * 4 + DEC_N * 4
-
-# HBM bytes per decode launch, from two rocprofv3 --pmc passes over
-# ``bench.py --no-cpu --no-prefill`` (FETCH_SIZE, then WRITE_SIZE, KiB per
-# dispatch), each scaled by what the same counter reads for a 512 MiB device
-# copy (``--copy-calibration 512``): FETCH_SIZE reads 262156.8 KiB for the
-# copy's 524288 KiB of reads (scale 2.0), WRITE_SIZE reads 524288 KiB (1.0).
-# The kernel-trace/PMC summaries are kept under profiles/.
-FETCH_SCALE = 524288.0 / 262156.8
-WRITE_SCALE = 524288.0 / 524288.0
-DEC_FETCH_KIB, DEC_WRITE_KIB = 267449.1, 526336.1
-DEC_TRAFFIC = (DEC_FETCH_KIB * FETCH_SCALE + DEC_WRITE_KIB * WRITE_SCALE) * 1024
-# Same for config 5's 4-token verify launch (1024 sequences, H=16).
-VF_TRAFFIC = (565882.7 * FETCH_SCALE + 1063961.9 * WRITE_SCALE) * 1024
-# Same for the two prefill kernels (prepare K1, scan K2) on config 3.
-PF_TRAFFIC = ((168225.2 + 223851.4) * FETCH_SCALE + (444972.4 + 124021.7) * WRITE_SCALE) * 1024
-# MFMA counters of the same two kernels (profiles/prefill_chunk_t8192_h32_mfma.md): matrix work
-# executed per call (SQ_INSTS_VALU_MFMA_MOPS_* x 512 FLOP; the hi/lo operand splits roughly
-# double the algorithmic count) and the fraction of SIMD cycles each kernel keeps the MFMA busy.
-PF_MFMA_EXECUTED_FLOP = (39845888 + 69206016 + 50331648 + 1048576) * 512
-PF_MFMA_BUSY = {"prepare": 28311552 / (3707468 / 8 * 1024), "scan": 59768832 / (3466918 / 8 * 1024)}
 
 # Config 3 (prefill) shape.
 PF_T, PF_H, PF_D, PF_BT = 8192, 32, 128, 64
 # Dense-tile FLOPs per token-head: 2*(5*BT*D + 3*D*D).
-PF_FLOP = PF_T * PF_H * 2 * (5 * PF_BT * PF_D + 3 * PF_D * PF_D)
-# Algorithmic bytes: q,k,v bf16 in, g fp32, beta fp32, o bf16 out, final state fp32 out.
-PF_BYTES = PF_T * PF_H * (3 * PF_D * 2 + PF_D * 4 + 4 + PF_D * 2) + PF_H * PF_D * PF_D * 4
+FLOP_PER_TOKEN_HEAD = 2 * (5 * PF_BT * PF_D + 3 * PF_D * PF_D)
+PF_FLOP = PF_T * PF_H * FLOP_PER_TOKEN_HEAD
+# q,k,v bf16 in, g fp32, beta fp32, o bf16 out, per token row.
+BYTES_PER_TOKEN_ROW = 3 * 128 * 2 + 128 * 4 + 4 + 128 * 2
+# Algorithmic bytes: the token rows plus the final state written (zero initial state).
+PF_BYTES = PF_T * PF_H * BYTES_PER_TOKEN_ROW + PF_H * PF_D * PF_D * 4
+
+# Reference 910B4 latencies (ms) at the same shapes, for context only:
+# bench/kda_recurrent/DISCARDED-cann-recurrent-kda.md:22-30 (decode, eager call)
+# and kda_varlen_recurrent_decode_h32.cpp:760-765 (verify R2, kernel only).
+REF_910B4_MS = {
+    "decode H16 B1": 0.121, "decode H16 B32": 0.133, "decode H16 B128": 0.303,
+    "decode H32 B1": 0.118, "decode H32 B32": 0.146, "decode H32 B128": 0.633,
+    "decode H64 B1": 0.140, "decode H64 B32": 0.301, "decode H64 B128": 1.225,
+    "verify 256K DP4TP2 R2": 0.03698,
+}
 
 
 def _log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def decode_inputs(device):
+# ---------------------------------------------------------------------------
+# timing
+# ---------------------------------------------------------------------------
+
+
+def _batch_us(step, n):
+    """Mean HIP-event time per call over ``n`` back-to-back calls on the
+    current stream (the stream the operators launch on)."""
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(n):
+        step()
+    ev1.record(stream)
+    ev1.synchronize()
+    return ev0.elapsed_time(ev1) * 1e3 / n
+
+
+def settle(step, min_calls, max_calls=2000, batch=10, rel=0.01):
+    """Run ``step`` until two successive 10-call batch means agree within
+    ``rel`` and at least ``min_calls`` calls ran (a fresh box's clocks and
+    translation caches take a few hundred microseconds of work to settle).
+    Returns the number of calls made."""
+    calls = 0
+    prev = None
+    while calls < max_calls:
+        cur = _batch_us(step, batch)
+        calls += batch
+        if prev is not None and calls >= min_calls and abs(cur - prev) <= rel * prev:
+            break
+        prev = cur
+    return calls
+
+
+def timed(step, steps, warmup, min_settle):
+    """Settle, ``warmup`` untimed calls, then ``steps`` timed calls bracketed by
+    device synchronization. Returns wall ms per call, HIP-event µs per call on
+    the launch stream, and the settle call count."""
+    settle_calls = settle(step, min_settle)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return dict(ms_per_step=(t1 - t0) * 1e3 / steps,
+                event_us_per_call=ev0.elapsed_time(ev1) * 1e3 / steps,
+                settle_calls=settle_calls)
+
+
+# ---------------------------------------------------------------------------
+# committed profile figures
+# ---------------------------------------------------------------------------
+
+
+def source_sha256(names=("kda_recurrent.hip", "kda_chunk.hip", "kda_device.h")):
+    """sha256 over the kernel sources, in order (the key the profile summaries
+    record, so a figure measured on other kernels is never reported)."""
+    h = hashlib.sha256()
+    for n in names:
+        with open(os.path.join(CSRC, n), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def profile_figures(name):
+    """The ``bench-figures: {...}`` JSON line of ``profiles/<name>`` or None."""
+    path = os.path.join(PROFILES, name)
+    try:
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*bench-figures:\s*(\{.*\})\s*$", line)
+                if m:
+                    return json.loads(m.group(1))
+    except OSError:
+        return None
+    return None
+
+
+def traffic_from_profile(name, source):
+    """HBM bytes per launch from a counter summary: FETCH_SIZE and WRITE_SIZE
+    KiB per dispatch, each scaled by what the same counter reads for a device
+    copy of known size. None (and the reason) when the summary is missing or
+    was measured on other kernel sources."""
+    fig = profile_figures(name)
+    if fig is None:
+        return None, f"no bench-figures line in profiles/{name}"
+    if fig.get("source_sha256") != source:
+        return None, (f"profiles/{name} was measured on kernel sources "
+                      f"{fig.get('source_sha256')}, these are {source}")
+    fs = fig["copy_bytes_kib"] / fig["copy_fetch_kib"]
+    ws = fig["copy_bytes_kib"] / fig["copy_write_kib"]
+    return (fig["fetch_kib"] * fs + fig["write_kib"] * ws) * 1024, f"profiles/{name}"
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+
+def decode_case():
+    """BASELINE config 2 on the CPU (seeded), the permutation drawn with seed 2."""
     from tests import kda_cases as C
 
     perm = torch.randperm(DEC_SLOTS, generator=C.gen(2))[:DEC_N].tolist()
-    case = C.prepared_case(DEC_H, (1,) * DEC_N, D=DEC_D, slots=DEC_SLOTS, indices=perm, seed=2)
-    return case
+    return C.prepared_case(DEC_H, (1,) * DEC_N, D=DEC_D, slots=DEC_SLOTS, indices=perm, seed=2)
 
 
-def run_decode(steps, warmup, device="cuda"):
+def prefill_case():
+    """BASELINE config 3 on the CPU: T=8192, H=32, zero initial state in slot 1
+    (slot 2 is spare: the validation call tracks a prefix into it)."""
     from tests import kda_cases as C
 
-    ops = torch.ops.sgl_glm53_ascend
-    case = decode_inputs(device)
-    q, k, v, g, beta = (getattr(case, n).to(device) for n in ("q", "k", "v", "g", "beta"))
-    pool = C.to_dev(case.pool, device)
-    idx = case.indices.to(device)
-    cu = case.cu_seqlens.to(device)
-
-    def step():
-        return ops.kda_prepared_varlen_recurrent(
-            q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
-            cu_seqlens=cu, scale=case.scale)
-
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / steps
-    kernel_us = ev0.elapsed_time(ev1) * 1e3 / steps
-    return dict(ms_per_step=ms_step, kernel_us=kernel_us)
-
-
-def run_prefill(steps, warmup, device="cuda"):
-    from tests import kda_cases as C
-
-    ops = torch.ops.sgl_glm53_ascend
-    case = C.prepared_case(PF_H, (PF_T,), D=PF_D, slots=2, indices=[1], seed=3, zero_pool=True)
-    q, k, v, g, beta = (getattr(case, n).to(device) for n in ("q", "k", "v", "g", "beta"))
-    pool = C.to_dev(case.pool, device)
-    idx = case.indices.to(device)
-    cu = case.cu_seqlens.to(device)
-
-    def step():
-        pool.zero_()  # zero initial state each step (config 3)
-        return ops.kda_prepared_varlen_chunk(
-            q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
-            cu_seqlens=cu, scale=case.scale)
-
-    try:
-        step()
-        torch.cuda.synchronize()
-    except RuntimeError as e:
-        _log(f"prefill unavailable: {str(e).splitlines()[0]}")
-        return None
-    for _ in range(warmup):
-        step()
-    stream = torch.cuda.current_stream()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / steps
-    gpu_us = ev0.elapsed_time(ev1) * 1e3 / steps
-    return dict(ms_per_step=ms_step, gpu_us=gpu_us)
-
-
-# Configs 4 and 5 (reported beside the headline, a few timed calls each).
-BYTES_PER_TOKEN_ROW = 3 * 128 * 2 + 128 * 4 + 4 + 128 * 2  # q,k,v bf16, g fp32, beta, o bf16
-FLOP_PER_TOKEN_HEAD = 2 * (5 * 64 * 128 + 3 * 128 * 128)
+    return C.prepared_case(PF_H, (PF_T,), D=PF_D, slots=3, indices=[1], seed=3, zero_pool=True)
 
 
 def _device_case(heads, lengths, *, slots, indices, seed, gate=(1.0, 0.0), zero_pool=False,
@@ -199,22 +251,7 @@ def _device_case(heads, lengths, *, slots, indices, seed, gate=(1.0, 0.0), zero_
                 cu=torch.tensor(cu, dtype=torch.int32, device=device), scale=D ** -0.5)
 
 
-def _time(step, steps, warmup):
-    for _ in range(warmup):
-        step()
-    stream = torch.cuda.current_stream()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    for _ in range(steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    return ev0.elapsed_time(ev1) * 1e3 / steps
-
-
-def run_more(steps=5, warmup=1):
+def run_more(steps, warmup):
     """Configs 4 and 5 prefill, and config 5's 4-token decode, on the device."""
     from tests import kda_cases as C
 
@@ -232,12 +269,14 @@ def run_more(steps=5, warmup=1):
                 c["q"], c["k"], c["v"], c["g"], c["beta"], initial_state_source=c["pool"],
                 initial_state_indices=c["idx"], cu_seqlens=c["cu"], scale=c["scale"])
 
-        us = _time(step, steps, warmup)
+        r = timed(step, steps, warmup, 30)
+        us = r["event_us_per_call"]
         flop = T * heads * FLOP_PER_TOKEN_HEAD
         state_bytes = N * heads * 128 * 128 * 4 * (1 if zero_pool else 2)
         nbytes = T * heads * BYTES_PER_TOKEN_ROW + state_bytes
         tf = flop / (us * 1e-6) / 1e12
-        out[name] = dict(tokens=T, heads=heads, seqs=N, gpu_us=us, tok_per_s=T / (us * 1e-6),
+        out[name] = dict(tokens=T, heads=heads, seqs=N, event_us_per_call=us,
+                         settle_calls=r["settle_calls"], tok_per_s=T / (us * 1e-6),
                          tflops=tf, mfma_frac=tf / BF16_PEAK_TFLOPS,
                          attainable_frac=(tf * 1e12) / min(BF16_PEAK_TFLOPS * 1e12,
                                                            HBM_PEAK_GBS * 1e9 * flop / nbytes),
@@ -261,117 +300,266 @@ def run_more(steps=5, warmup=1):
             c["q"], c["k"], c["v"], c["g"], c["beta"], initial_state_source=c["pool"],
             initial_state_indices=c["idx"], cu_seqlens=c["cu"], scale=c["scale"])
 
-    us = _time(dstep, max(steps, 10), max(warmup, 2))
+    r = timed(dstep, max(steps, 10), warmup, 60)
+    us = r["event_us_per_call"]
     nbytes = (n5 * h5 * 2 * 128 * 128 * 4 + n5 * steps5 * h5 * BYTES_PER_TOKEN_ROW
               + (n5 + 1) * 4 + n5 * 4)
     gbs = nbytes / (us * 1e-6) / 1e9
     out["config5_decode"] = dict(seqs=n5, tokens_per_seq=steps5, heads=h5, pool_slots=slots5,
-                                 kernel_us=us, tok_per_s=n5 * steps5 / (us * 1e-6),
+                                 event_us_per_call=us, settle_calls=r["settle_calls"],
+                                 tok_per_s=n5 * steps5 / (us * 1e-6),
                                  hbm_gbs=gbs, hbm_frac=gbs / HBM_PEAK_GBS,
-                                 algorithmic_bytes=nbytes, traffic=VF_TRAFFIC,
-                                 kernel="recurrent_kernel<128,16,8,consecutive rows,multi-token>")
+                                 algorithmic_bytes=nbytes)
     _log(f"config5_decode: {us:.1f} us, {gbs:.0f} GB/s")
     return out
 
 
-def cpu_baseline(budget_s=10.0):
+# ---------------------------------------------------------------------------
+# the CPU baseline leg: the oracle timed on the host, and as the checker
+# ---------------------------------------------------------------------------
+
+
+def _median_time(fn, budget_s, max_runs):
+    fn()  # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_decode(case, sample_n=64, budget_s=10.0):
     """The oracle's recurrent decode (the reference CPU path's loop structure,
-    bench/kda_chunk/kda_python.py:253-307) on the host cores."""
+    bench/kda_chunk/kda_python.py:253-307) on the first ``sample_n`` of the
+    config-2 sequences, on the host cores. Returns the baseline figures and the
+    oracle's outputs and states (the checker's reference for those sequences):
+    their slots are renumbered 1..sample_n in a compact pool (0 stays 0)."""
+    from oracle import kda_ref as R
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    perm = case.indices[:sample_n].tolist()
+    D = case.q.shape[-1]
+    pool0 = torch.zeros(sample_n + 1, DEC_H, D, D).transpose(-1, -2)
+    idx = []
+    for i, s in enumerate(perm):
+        if s > 0:
+            pool0[i + 1] = case.pool[s]
+        idx.append(i + 1 if s > 0 else 0)
+    idx = torch.tensor(idx, dtype=torch.int32)
+    cu = torch.arange(sample_n + 1, dtype=torch.int32)
+    qs = case.q[:, :sample_n].float() * case.scale
+    k, v, g, beta = (t[:, :sample_n] for t in (case.k, case.v, case.g, case.beta))
+    box = {}
+
+    def once():
+        pool = pool0.transpose(-1, -2).clone().transpose(-1, -2)
+        box["out"] = R.kda_recurrent(qs, k, v, g, beta, state_pool=pool, state_indices=idx,
+                                     cu_seqlens=cu, out_dtype=torch.float32)
+        box["pool"] = pool
+
+    med, runs = _median_time(once, budget_s, 50)
+    base = dict(value=sample_n / med, unit="tok/s", cores=torch.get_num_threads(), kind="port",
+                sample=(f"oracle kda_recurrent (torch fp32, CPU) on {sample_n} of the 256 "
+                        f"config-2 sequences x 1 token, H={DEC_H}, K=V={DEC_D}; median of "
+                        f"{runs} runs; os.cpu_count()={os.cpu_count()}"))
+    return base, box["out"], box["pool"], idx
+
+
+def cpu_prefill(case, sample_t=512, budget_s=12.0):
+    """The oracle's chunked prefill (bench/kda_chunk/kda_python.py:41-188) on
+    the first ``sample_t`` of the config-3 tokens, all heads, on the host
+    cores. Returns the baseline figures, the oracle's output and its state
+    after the sample (the checker's reference for the same prefix)."""
+    from oracle import kda_ref as R
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    qs = case.q[:, :sample_t].float() * case.scale
+    k, v, g, beta = (t[:, :sample_t] for t in (case.k, case.v, case.g, case.beta))
+    D = case.q.shape[-1]
+    box = {}
+
+    def once():
+        pool = torch.zeros(2, PF_H, D, D).transpose(-1, -2)
+        box["out"] = R.kda_chunk(qs, k, v, g, beta, state_pool=pool,
+                                 state_indices=torch.tensor([1], dtype=torch.int32),
+                                 cu_seqlens=torch.tensor([0, sample_t], dtype=torch.int32),
+                                 out_dtype=torch.float32)
+        box["state"] = pool[1].clone()
+
+    med, runs = _median_time(once, budget_s, 20)
+    base = dict(value=sample_t / med, unit="tok/s", cores=torch.get_num_threads(), kind="port",
+                sample=(f"oracle kda_chunk (torch fp32, CPU, chunk 64) on the first {sample_t} "
+                        f"of the 8192 config-3 tokens, H={PF_H}, K=V={PF_D}; median of {runs} "
+                        f"runs; os.cpu_count()={os.cpu_count()}"))
+    return base, box["out"], box["state"]
+
+
+def _errs(out, ref_out, state, ref_state):
+    from tests import kda_cases as C
+
+    return dict(out_err=C.out_err(out, ref_out), state_err=C.max_rel_err(state, ref_state))
+
+
+def _passed(v):
+    from tests import kda_cases as C
+
+    return v["out_err"] <= C.OUT_TOL and v["state_err"] <= C.STATE_TOL
+
+
+# ---------------------------------------------------------------------------
+# latency rows (the reference bench's deployed shapes)
+# ---------------------------------------------------------------------------
+
+
+def latency_regimes():
+    """(label, heads, lengths, prefill, checkpoints), as the reference bench's
+    ``regimes()`` (bench_kda_varlen_recurrent.py:534-551) with its constants
+    (:77-114): decode H16/32/64 x B1/32/128; the verify shapes with 4 draft
+    tokens per request, checkpointed; recurrent prefill H4/H8 x T1k-16k."""
+    for heads in (16, 32, 64):
+        for batch in (1, 32, 128):
+            yield f"decode H{heads} B{batch}", heads, (1,) * batch, False, False
+    for label, heads, req in (("256K DP4TP2", 32, 2), ("256K DP2TP4", 16, 3),
+                              ("256K DP8TP1", 64, 1), ("512K DP4TP2", 32, 1),
+                              ("512K DP2TP4", 16, 1)):
+        yield f"verify {label} R{req}", heads, (4,) * req, False, True
+    for heads in (4, 8):
+        for tokens in (1024, 2048, 4096, 8192, 16384):
+            yield f"prefill H{heads} T{tokens // 1024}k", heads, (tokens,), True, False
+
+
+def run_latency_rows(steps, check):
+    """Each regime through the sglang-facing op (raw gates, the reference
+    bench's distributions), validated against the oracle when ``check`` (the
+    CPU leg is on), then timed."""
     from oracle import kda_ref as R
     from tests import kda_cases as C
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    sample_n = 64
-    case = C.prepared_case(DEC_H, (1,) * sample_n, D=DEC_D, slots=sample_n + 1, seed=2)
-    qs = case.q.float() * case.scale
+    ops = torch.ops.sgl_glm53_ascend
+    rows = []
+    for label, heads, lengths, prefill, ckpt in latency_regimes():
+        case = C.raw_case(heads, lengths, seed=1000 + heads + len(lengths) + sum(lengths))
+        N = len(lengths)
+        D = 128
+        mid = None
+        if ckpt:
+            mid = (torch.randn(N, max(lengths), heads, D, D) * 0.1).transpose(-1, -2)
+        pool = C.to_dev(case.pool, "cuda")
+        mid_d = None if mid is None else mid.transpose(-1, -2).contiguous().cuda().transpose(-1, -2)
+        kw = case.kwargs("cuda", pool=pool)
 
-    def once():
-        pool = C.clone_pool(case.pool)
-        t0 = time.perf_counter()
-        R.kda_recurrent(qs, case.k, case.v, case.g, case.beta, state_pool=pool,
-                        state_indices=case.indices, cu_seqlens=case.cu_seqlens)
-        return time.perf_counter() - t0
+        def step():
+            return ops.kda_varlen_recurrent(intermediate_state=mid_d, prefill=prefill, **kw)
 
-    once()  # warm-up
-    times = []
-    start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 50):
-        times.append(once())
-    med = statistics.median(times)
-    return dict(
-        value=sample_n / med,
-        unit="tok/s",
-        cores=torch.get_num_threads(),
-        kind="port",
-        sample=(f"oracle kda_recurrent (torch fp32, CPU) on {sample_n} of the 256 config-2 "
-                f"sequences x 1 token, H={DEC_H}, K=V={DEC_D}; median of {len(times)} runs; "
-                f"os.cpu_count()={os.cpu_count()}"),
-    )
-
-
-def cpu_baseline_prefill(budget_s=12.0):
-    """The oracle's chunked prefill (the reference CPU path's structure,
-    bench/kda_chunk/kda_python.py:41-188) on the host cores, over a bounded
-    sample of config 3: the first 512 of its 8192 tokens, all 32 heads."""
-    from oracle import kda_ref as R
-    from tests import kda_cases as C
-
-    torch.set_num_threads(os.cpu_count() or 1)
-    sample_t = 512
-    case = C.prepared_case(PF_H, (sample_t,), D=PF_D, slots=2, indices=[1], seed=3,
-                           zero_pool=True)
-    qs = case.q.float() * case.scale
-
-    def once():
-        pool = C.clone_pool(case.pool)
-        t0 = time.perf_counter()
-        R.kda_chunk(qs, case.k, case.v, case.g, case.beta, state_pool=pool,
-                    state_indices=case.indices, cu_seqlens=case.cu_seqlens)
-        return time.perf_counter() - t0
-
-    once()  # warm-up
-    times = []
-    start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 20):
-        times.append(once())
-    med = statistics.median(times)
-    return dict(
-        value=sample_t / med,
-        unit="tok/s",
-        cores=torch.get_num_threads(),
-        kind="port",
-        sample=(f"oracle kda_chunk (torch fp32, CPU, chunk 64) on the first {sample_t} of the "
-                f"8192 config-3 tokens, H={PF_H}, K=V={PF_D}; median of {len(times)} runs; "
-                f"os.cpu_count()={os.cpu_count()}"),
-    )
+        row = dict(label=label, heads=heads, requests=N, tokens=int(sum(lengths)))
+        if check:
+            out = step()
+            torch.cuda.synchronize()
+            ref_pool = C.clone_pool(case.pool)
+            ref_mid = None if mid is None else mid.transpose(-1, -2).clone().transpose(-1, -2)
+            qn, kn, g, beta = R.kda_prepare(case.A_log, case.a, case.dt_bias, case.q, case.k,
+                                            case.b, case.lower_bound, case.scale)
+            ref = R.kda_recurrent(qn, kn, case.v, g, beta, state_pool=ref_pool,
+                                  state_indices=case.indices, cu_seqlens=case.cu_seqlens,
+                                  intermediate_state=ref_mid, out_dtype=torch.float32)
+            v = _errs(out.cpu(), ref, pool.cpu(), ref_pool)
+            if ref_mid is not None:
+                v["checkpoint_err"] = C.max_rel_err(mid_d.cpu(), ref_mid)
+            v["passed"] = _passed(v) and v.get("checkpoint_err", 0.0) <= C.STATE_TOL
+            row["validated"] = v
+        r = timed(step, steps, 2, 30)
+        us = r["event_us_per_call"]
+        T = int(sum(lengths))
+        # state in + out per (sequence, head) (the checkpoints are written
+        # instead of the final state), plus the token rows (raw gates: q, k,
+        # v, a bf16 in, b bf16, o bf16 out)
+        state_bytes = N * heads * D * D * 4 * (1 + (max(lengths) if ckpt else 1))
+        nbytes = state_bytes + T * heads * (5 * D * 2 + 2)
+        row.update(event_us_per_call=us, settle_calls=r["settle_calls"],
+                   hbm_gbs=nbytes / (us * 1e-6) / 1e9, algorithmic_bytes=nbytes,
+                   ref_910b4_ms=REF_910B4_MS.get(label))
+        rows.append(row)
+        ok = row.get("validated", {}).get("passed", True)
+        _log(f"{label}: {us:.1f} us, {row['hbm_gbs']:.0f} GB/s{'' if ok else '  VALIDATION FAILED'}")
+    return rows
 
 
-def _prefill_steps(args):
-    """(steps, warmup) for the config-3 prefill: half the decode step count and
-    the decode's warm-up count. On a fresh box the decode settles after ~150
-    calls (~25 ms: 188 -> 173 us per call) and the prefill after ~100 (~40 ms:
-    449 -> 381 us), hence the default of 200 warm-up calls."""
-    return max(3, args.steps // 2), max(1, args.warmup)
+# ---------------------------------------------------------------------------
+# profile summaries
+# ---------------------------------------------------------------------------
+
+
+def summarize_trace(path, last):
+    """Per-kernel duration statistics from a rocprofv3 kernel-trace CSV over
+    each kernel's last ``last`` dispatches (0 = all)."""
+    by = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            us = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
+            by.setdefault(row["Kernel_Name"], []).append((int(row["Dispatch_Id"]), us))
+    print(f"| kernel | dispatches | used | mean µs | median µs | min µs | max µs |")
+    print("|---|---|---|---|---|---|---|")
+    for name, xs in sorted(by.items(), key=lambda kv: -sum(u for _, u in kv[1])):
+        xs.sort()
+        sel = [u for _, u in (xs[-last:] if last > 0 else xs)]
+        print(f"| `{name[:110]}` | {len(xs)} | {len(sel)} | {statistics.mean(sel):.2f} | "
+              f"{statistics.median(sel):.2f} | {min(sel):.2f} | {max(sel):.2f} |")
+
+
+def summarize_counters(path):
+    """Mean value per dispatch of every counter, per kernel, from a rocprofv3
+    counter-collection CSV."""
+    by = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            key = (row["Kernel_Name"], row["Counter_Name"])
+            by.setdefault(key, []).append(float(row["Counter_Value"]))
+    print("| kernel | counter | dispatches | mean per dispatch |")
+    print("|---|---|---|---|")
+    for (name, ctr), xs in sorted(by.items()):
+        print(f"| `{name[:110]}` | {ctr} | {len(xs)} | {statistics.mean(xs):.1f} |")
+
+
+# ---------------------------------------------------------------------------
+# main
+# ---------------------------------------------------------------------------
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle", type=int, default=150,
+                    help="minimum settle calls before the warm-up (decode; prefill: 2/3)")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU leg (baseline timing and the validation it checks)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill workload")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode workload")
     ap.add_argument("--no-more", action="store_true",
-                    help="skip the config 4 / 5 lines reported beside the headline")
+                    help="skip the config 4 / 5 lines and the latency rows")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (the known-size kernel "
                          "the FETCH_SIZE / WRITE_SIZE counters are scaled by), then exit")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print per-kernel durations from a rocprofv3 kernel-trace CSV, then exit")
+    ap.add_argument("--summarize-counters", metavar="CSV",
+                    help="print per-kernel counter means from a rocprofv3 counter CSV, then exit")
+    ap.add_argument("--last", type=int, default=0,
+                    help="with --summarize-trace: use each kernel's last N dispatches")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.last)
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
-              "(the KDA path shards by head and sequence with no exchange inside the op).",
-              file=sys.stderr)
+              "(the KDA path shards by head and sequence with no exchange inside the op; "
+              "this build runs and measures a single GPU).", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.copy_calibration > 0:
@@ -384,57 +572,128 @@ def main():
         _log(f"copy calibration: 5 x {args.copy_calibration} MiB device copies")
         return
     import sgl_glm53_ascend_ops  # noqa: F401
+    from tests import kda_cases as C
 
-    if args.no_decode:
-        # profiling aid: the prefill workload alone (no JSON line)
-        _log("prefill: config 3 (T=8192, H=32, K=V=128, chunk 64)")
-        pf = run_prefill(*_prefill_steps(args))
-        if pf is not None:
-            _log(f"prefill: {pf['ms_per_step']*1e3:.1f} us/step")
-        return
-    _log("decode: config 2 (B=256, H=32, K=V=128)")
-    dec = run_decode(args.steps, args.warmup)
-    tok_s = DEC_N / (dec["ms_per_step"] / 1e3)
-    achieved = DEC_BYTES / (dec["kernel_us"] * 1e-6) / 1e9
-    _log(f"decode: {dec['ms_per_step']*1e3:.1f} us/step, kernel {dec['kernel_us']:.1f} us, "
-         f"{achieved:.0f} GB/s")
+    ops = torch.ops.sgl_glm53_ascend
+    check = not args.no_cpu
+    sha = source_sha256()
+    validated = {}
+    failed = False
+
+    dec = None
+    cpu = None
+    if not args.no_decode:
+        _log("decode: config 2 (B=256, H=32, K=V=128)")
+        case = decode_case()
+        q, k, v, g, beta = (getattr(case, n).cuda() for n in ("q", "k", "v", "g", "beta"))
+        idx = case.indices.cuda()
+        cu = case.cu_seqlens.cuda()
+        if check:
+            pool = C.to_dev(case.pool, "cuda")
+            out = ops.kda_prepared_varlen_recurrent(q, k, v, g, beta, initial_state_source=pool,
+                                                    initial_state_indices=idx, cu_seqlens=cu,
+                                                    scale=case.scale)
+            torch.cuda.synchronize()
+            _log("cpu baseline / checker: oracle decode on host cores")
+            cpu, ref_out, ref_pool, sidx = cpu_decode(case)
+            n = ref_out.shape[1]
+            slots = case.indices[:n].tolist()
+            got_state = torch.stack([pool[s].cpu() if s > 0 else torch.zeros_like(ref_pool[0])
+                                     for s in slots])
+            ref_state = torch.stack([ref_pool[int(i)] for i in sidx.tolist()])
+            validated["decode"] = _errs(out[:, :n].cpu(), ref_out, got_state, ref_state)
+            validated["decode"]["sample"] = f"first {n} of {DEC_N} sequences"
+            ok = _passed(validated["decode"])
+            failed |= not ok
+            _log(f"decode validation: {validated['decode']}{'' if ok else '  FAILED'}")
+            _log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+            del pool
+        pool = C.to_dev(case.pool, "cuda")
+
+        def step():
+            return ops.kda_prepared_varlen_recurrent(
+                q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
+                cu_seqlens=cu, scale=case.scale)
+
+        dec = timed(step, args.steps, args.warmup, args.settle)
+        _log(f"decode: {dec['event_us_per_call']:.1f} us/call after {dec['settle_calls']} "
+             "settle calls")
+        del pool, case
 
     prefill = None
     if not args.no_prefill:
         _log("prefill: config 3 (T=8192, H=32, K=V=128, chunk 64)")
-        pf = run_prefill(*_prefill_steps(args))
-        if pf is not None:
-            tf = PF_FLOP / (pf["gpu_us"] * 1e-6) / 1e12
-            prefill = dict(
-                workload="chunk prefill T=8192 H=32 K=V=128 BT=64 bf16 qkv, fp32 g/beta/state",
-                tok_per_s=PF_T / (pf["ms_per_step"] / 1e3),
-                ms_per_step=pf["ms_per_step"],
-                gpu_us=pf["gpu_us"],
-                tflops=tf,
-                mfma_frac=tf / BF16_PEAK_TFLOPS,
-                hbm_gbs=PF_BYTES / (pf["gpu_us"] * 1e-6) / 1e9,
-                traffic=PF_TRAFFIC,
-                mfma_executed_tflops=PF_MFMA_EXECUTED_FLOP / (pf["gpu_us"] * 1e-6) / 1e12,
-                mfma_busy=PF_MFMA_BUSY,
-                attainable_frac=(tf * 1e12) / min(BF16_PEAK_TFLOPS * 1e12,
-                                                  HBM_PEAK_GBS * 1e9 * PF_FLOP / PF_BYTES),
-            )
-            _log(f"prefill: {pf['ms_per_step']*1e3:.1f} us/step, {tf:.1f} TFLOP/s")
+        case = prefill_case()
+        q, k, v, g, beta = (getattr(case, n).cuda() for n in ("q", "k", "v", "g", "beta"))
+        pool = C.to_dev(case.pool, "cuda")
+        idx = case.indices.cuda()
+        cu = case.cu_seqlens.cuda()
+        pf_cpu = None
+        if check:
+            sample_t = 512
+            out = ops.kda_prepared_varlen_chunk(
+                q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
+                cu_seqlens=cu, scale=case.scale,
+                track_state_indices=torch.tensor([2], dtype=torch.int32, device="cuda"),
+                track_state_lens=torch.tensor([sample_t], dtype=torch.int32, device="cuda"))
+            torch.cuda.synchronize()
+            _log("cpu baseline / checker: oracle chunked prefill on host cores")
+            pf_cpu, ref_out, ref_state = cpu_prefill(case, sample_t)
+            validated["prefill"] = _errs(out[:, :sample_t].cpu(), ref_out, pool[2].cpu(),
+                                         ref_state)
+            validated["prefill"]["sample"] = (f"first {sample_t} of {PF_T} tokens; state "
+                                              f"tracked at {sample_t}")
+            ok = _passed(validated["prefill"])
+            failed |= not ok
+            _log(f"prefill validation: {validated['prefill']}{'' if ok else '  FAILED'}")
+
+        def pstep():
+            pool[1].zero_()  # zero initial state each step (config 3)
+            return ops.kda_prepared_varlen_chunk(
+                q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
+                cu_seqlens=cu, scale=case.scale)
+
+        pf = timed(pstep, max(5, args.steps // 2), args.warmup, (2 * args.settle) // 3)
+        us = pf["event_us_per_call"]
+        tf = PF_FLOP / (us * 1e-6) / 1e12
+        traffic, traffic_src = traffic_from_profile("prefill_chunk_t8192_h32_hbm_traffic.md", sha)
+        prefill = dict(
+            workload="chunk prefill T=8192 H=32 K=V=128 BT=64 bf16 qkv, fp32 g/beta/state",
+            tok_per_s=PF_T / (pf["ms_per_step"] / 1e3),
+            ms_per_step=pf["ms_per_step"],
+            event_us_per_call=us,
+            settle_calls=pf["settle_calls"],
+            tflops=tf,
+            mfma_frac=tf / BF16_PEAK_TFLOPS,
+            attainable_frac=(tf * 1e12) / min(BF16_PEAK_TFLOPS * 1e12,
+                                              HBM_PEAK_GBS * 1e9 * PF_FLOP / PF_BYTES),
+            hbm_gbs=PF_BYTES / (us * 1e-6) / 1e9,
+            algorithmic_flop=PF_FLOP,
+            algorithmic_bytes=PF_BYTES,
+            traffic=traffic,
+            traffic_source=traffic_src,
+            workspace_bytes=int(sgl_glm53_ascend_ops.chunk_workspace_bytes(PF_T, 1, PF_H)),
+            cpu_baseline=pf_cpu,
+        )
+        _log(f"prefill: {us:.1f} us/call, {tf:.1f} TFLOP/s after {pf['settle_calls']} settle calls")
+        del pool, case
 
     more = None
+    rows = None
     if not args.no_more:
-        more = run_more(max(3, args.steps // 5), max(1, args.warmup // 4))
+        more = run_more(max(3, args.steps // 5), 2)
+        rows = run_latency_rows(10, check)
+        bad = [r["label"] for r in rows if not r.get("validated", {}).get("passed", True)]
+        if bad:
+            failed = True
+            _log(f"latency rows failing validation: {bad}")
+        validated["latency_rows"] = "all passed" if not bad else f"failed: {bad}"
 
-    cpu = None
-    if not args.no_cpu:
-        _log("cpu baseline: oracle decode on host cores")
-        cpu = cpu_baseline()
-        _log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
-        if prefill is not None:
-            _log("cpu baseline: oracle chunked prefill on host cores")
-            prefill["cpu_baseline"] = cpu_baseline_prefill()
-            _log(f"cpu baseline (prefill): {prefill['cpu_baseline']['value']:.1f} tok/s")
-
+    if dec is None:
+        return
+    tok_s = DEC_N / (dec["ms_per_step"] / 1e3)
+    achieved = DEC_BYTES / (dec["event_us_per_call"] * 1e-6) / 1e9
+    traffic, traffic_src = traffic_from_profile("decode_recurrent_b256_h32_hbm_traffic.md", sha)
     line = dict(
         metric="KDA decode tok/s + state HBM GB/s (B=256); chunk prefill tok/s (T=8k)",
         value=tok_s,
@@ -442,6 +701,7 @@ def main():
         n_gpus=1,
         steps=args.steps,
         warmup=args.warmup,
+        settle_calls=dec["settle_calls"],
         ms_per_step=dec["ms_per_step"],
         higher_is_better=True,
         scaling="weak",
@@ -454,18 +714,25 @@ def main():
                       "updated in place (BASELINE configs[1])"),
             batch=DEC_N, heads=DEC_H, head_dim=DEC_D, pool_slots=DEC_SLOTS,
         ),
+        validated=validated if check else None,
         state_hbm_gbs=achieved,
         roofline=dict(
             bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
-            frac=achieved / HBM_PEAK_GBS, traffic=DEC_TRAFFIC,
+            frac=achieved / HBM_PEAK_GBS, traffic=traffic, traffic_source=traffic_src,
             kernel="recurrent_kernel<128,32,2,strided rows,decode,bf16,bf16,LOG>",
-            algorithmic_bytes_per_launch=DEC_BYTES, kernel_us=dec["kernel_us"],
+            algorithmic_bytes_per_launch=DEC_BYTES,
+            event_us_per_call=dec["event_us_per_call"],
+            source_sha256=sha,
         ),
         prefill=prefill,
         more_configs=more,
+        latency_rows=rows,
         cpu_baseline=cpu,
     )
     print(json.dumps(line), flush=True)
+    if failed:
+        _log("validation failed: the figures above are not valid")
+        sys.exit(1)
 
 
 if __name__ == "__main__":

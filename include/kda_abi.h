@@ -10,14 +10,14 @@
  *   kda_recurrent_launch  replaces LaunchKdaDecodeH16/H32/H64 and
  *                         LaunchKdaPrefillH4/H8
  *                         (sgl-glm53-ascend-ops/csrc/kda/recurrent/
- *                          kda_varlen_recurrent.h:363-367), with the argument
- *                         block KdaLaunchArgs (same file, :328-361), and the
+ *                          kda_varlen_recurrent.h:94-98), with the argument
+ *                         block KdaLaunchArgs (same file, :59-92), and the
  *                         prepared-input kernels behind prepared_recurrent
  *                         (csrc/kda/prepared_recurrent.cpp:592-602,676-708);
- *   kda_chunk_launch      replaces LaunchKdaVarlenChunk
- *                         (csrc/kda/chunk/kda_varlen_chunk_kernel.cpp:1641-1662),
- *                         argument block KdaChunkLaunchArgs
- *                         (csrc/kda/chunk/kda_varlen_chunk.h:120-141);
+ *   kda_chunk_launch      replaces LaunchKdaVarlenChunk (declared at
+ *                         csrc/kda/chunk/kda_varlen_chunk.h:143, defined at
+ *                         kda_varlen_chunk_kernel.cpp:1641-1662), argument
+ *                         block KdaChunkLaunchArgs (kda_varlen_chunk.h:120-141);
  *   kda_chunk_workspace_bytes  sizes the chunk op's scratch, the analogue of
  *                         kWorkspaceFloatsPerBlock (kda_varlen_chunk.h:79-116).
  *
@@ -72,7 +72,9 @@ typedef enum KdaDType {
  *          kda_varlen_recurrent.cpp:257-265);
  *   LOG    gate = fp32 log decay g [T,H,D] (<= 0), beta = fp32 [T,H];
  *   DECAY  gate = fp32 multiplicative decay exp(g) [T,H,D], beta = fp32 [T,H]
- *          (the prepared_recurrent schema, prepared_recurrent.cpp:715-720). */
+ *          (the prepared_recurrent schema, prepared_recurrent.cpp:715-720);
+ *          `out` is caller-owned and only the rows the requests cover are
+ *          written (RAW and LOG also zero the rows no request covers). */
 typedef enum KdaGateMode {
     KDA_GATE_RAW = 0,
     KDA_GATE_LOG = 1,
@@ -95,7 +97,7 @@ typedef struct KdaRecurrentArgs {
 
     const int32_t *state_indices; /* [N] */
     const int32_t *cu_seqlens;    /* [N+1] */
-    void *out;                    /* [T,H,D], v_dtype; every token written */
+    void *out;                    /* [T,H,D], v_dtype; every token written (DECAY: covered rows only) */
 
     /* Per-step checkpoints [rows, steps, H, K, V], K contiguous (null = off).
      * Row = the request's position n, step = its local token index; written

@@ -128,6 +128,13 @@ def kda_recurrent(
     * ``intermediate_state[n, t] = S`` after every step when ``slot > 0``,
       indexed by the sequence's position ``n`` and its local step ``t``
       (:299-300);
+    * token inputs are read at their packed positions ``bos + t``. The anchor
+      itself indexes ``decay[:, t]``, ``kn[:, t]``, ``v[:, t]``, ``beta[:, t]``
+      and ``qn[:, t]`` with the sequence-local ``t`` (:276-303) while it writes
+      ``output[:, i]`` at the packed ``i``, which reads the first sequence's
+      tokens for every later one; the reference kernel reads packed rows
+      (kda_varlen_recurrent_decode_h32.cpp:393,595), and so does this
+      restatement (pinned by chunk == recurrent on multi-sequence batches);
     * the final write-back ``pool[slot] = S`` happens only when ``slot > 0``
       and no ``intermediate_state`` is given (:305-307).
 
@@ -351,48 +358,41 @@ def kda_varlen_chunk_ref(
 
 def prepared_recurrent_ref(
     qn, kn, v, gdecay, beta, out, state, indices, starts,
-    track_indices=None, track_lens=None, track_state=False,
+    track_indices=None, track_lens=None, track_state=False, head_offset=0,
     dtype: torch.dtype = torch.float32,
 ):
     """The ``prepared_recurrent`` op's recurrence (multiplicative decay input).
 
     Follows the prepared-gate recurrence stated in
-    bench/_prepared_recurrent/bench_prepared_recurrent.py:84-121: ``qn``/``kn``
-    fp32 already normalized (``qn`` scaled), ``gdecay = exp(g)``; the final
-    state is written back when ``slot > 0`` (:120-121). ``qn, kn, v, gdecay`` are ``[T*H, D]`` or ``[1, T, H, D]``;
-    ``beta`` is ``[T*H]`` or ``[1, T, H]``. Writes ``out`` in place.
+    bench/_prepared_recurrent/bench_prepared_recurrent.py:84-121 and the
+    Ascend launcher (sgl-glm53-ascend-ops/csrc/kda/prepared_recurrent.cpp:
+    620-707): ``qn``/``kn`` fp32 already normalized (``qn`` scaled),
+    ``gdecay = exp(g)``; one launch covers the four heads
+    ``[head_offset, head_offset + 4)`` (:629-634, program id 2 offset by
+    ``HEAD_OFFSET`` at bench_prepared_recurrent.py:84); each request ``n``
+    covers rows ``[starts[n], starts[n+1])`` and only those rows of those
+    heads are written to ``out`` (:117-118); the final state is written back
+    when ``slot > 0`` (:120-121). ``qn, kn, v, gdecay`` are ``[T*H, D]`` or
+    ``[1, T, H, D]``; ``beta`` is ``[T*H]`` or ``[1, T, H]``. Writes ``out``
+    and ``state`` in place.
     """
     H = state.shape[1]
     D = state.shape[2]
     T = qn.numel() // (H * D)
     shp = (1, T, H, D)
+    heads = list(range(head_offset, min(head_offset + 4, H)))
+    sub = lambda x: x.reshape(shp)[:, :, heads]  # noqa: E731
+    pool = state[:, heads]
     o = kda_recurrent(
-        qn.reshape(shp), kn.reshape(shp), v.reshape(shp), None,
-        beta.reshape(1, T, H),
-        state_pool=state, state_indices=indices, cu_seqlens=starts,
+        sub(qn), sub(kn), sub(v), None, beta.reshape(1, T, H)[:, :, heads],
+        state_pool=pool, state_indices=indices, cu_seqlens=starts,
         track_state_indices=track_indices if track_state else None,
         track_state_lens=track_lens if track_state else None,
-        dtype=dtype, decay=gdecay.reshape(shp),
+        dtype=dtype, decay=sub(gdecay),
     )
-    out.copy_(o.reshape(out.shape).to(out.dtype))
+    state[:, heads] = pool
+    o4 = out.view(shp)
+    cu = _as_list(starts)
+    for n in range(len(cu) - 1):
+        o4[:, cu[n]:cu[n + 1], heads] = o[:, cu[n]:cu[n + 1]].to(out.dtype)
     return None
-
-
-# ---------------------------------------------------------------------------
-# tolerance metric
-# ---------------------------------------------------------------------------
-
-
-def max_rel_err(x: torch.Tensor, ref: torch.Tensor) -> float:
-    """``max|x - ref| / max|ref|`` over the whole tensor (0 if ``ref`` is 0).
-
-    The per-tensor relative metric the tolerance contract is stated in:
-    per-element relative error is ill-conditioned on outputs near zero.
-    """
-    x = x.double()
-    ref = ref.double()
-    den = ref.abs().max().item()
-    num = (x - ref).abs().max().item()
-    if den == 0.0:
-        return num
-    return num / den

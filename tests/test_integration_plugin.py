@@ -1,6 +1,6 @@
 """sglang integration pieces on the CPU: the plugin hook and the op-then-fallback
-dispatcher (reference: src/sgl_glm53_ascend_ops/plugin.py:1-36,
-tests/integration/kda_ascendc_dispatch.py:52-101).
+dispatcher (reference: src/sgl_glm53_ascend_ops/plugin.py:1-35,
+tests/integration/kda_ascendc_dispatch.py:52-96).
 
 sglang is not installed, so its ``HookRegistry`` is replaced by a recording
 stand-in module; no kernel runs here.

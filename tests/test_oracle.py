@@ -23,6 +23,7 @@ import pytest
 import torch
 
 from oracle import kda_ref as R
+from tests import kda_cases as C
 
 F64 = torch.float64
 
@@ -281,8 +282,8 @@ def test_fp32_oracle_close_to_f64():
     o64 = R.kda_chunk(q, k, v, g, beta, state_pool=p64, state_indices=idx, cu_seqlens=cu, dtype=F64)
     o32 = R.kda_chunk(*(t.float() for t in (q, k, v, g, beta)), state_pool=p32,
                       state_indices=idx, cu_seqlens=cu, dtype=torch.float32)
-    assert R.max_rel_err(o32, o64) < 1e-5
-    assert R.max_rel_err(p32, p64) < 1e-5
+    assert C.max_rel_err(o32, o64) < 1e-5
+    assert C.max_rel_err(p32, p64) < 1e-5
 
 
 def test_raw_wrappers_agree():
@@ -317,3 +318,74 @@ def test_planted_mistake_is_caught():
     expect = (q[0, 0] * k[0, 0]).sum(-1, keepdim=True) * v[0, 0]
     assert not torch.allclose(o_wrong, expect)
     assert math.isfinite(float(expect.abs().sum()))
+
+
+# --- prepared_recurrent_ref (the prepared_recurrent op's oracle) -------------
+
+
+def _prepared_rec_inputs(T, H, D, seed):
+    q, k, v, g, beta = _prepared_inputs(T, H, D, seed)
+    flat = lambda x: x.reshape(T * H, D).clone()  # noqa: E731
+    return flat(q), flat(k), flat(v), flat(g.exp()), beta.reshape(T * H).clone(), g
+
+
+def test_prepared_recurrent_ref_equals_log_form():
+    """Two launches (heads 0-3, then 4-7) with multiplicative decays equal the
+    log-gate recurrence over all eight heads, outputs, pool and tracked slot,
+    in float64 -- a wrong head offset, a decay taken as a log, or a head range
+    that is not advanced would each break it."""
+    T, H, D = 23, 8, 16
+    qn, kn, v, dec, beta, g = _prepared_rec_inputs(T, H, D, seed=41)
+    starts = torch.tensor([0, 9, 23])
+    idx = torch.tensor([2, 0])  # the second request starts from the padding slot
+    tr_i, tr_l = torch.tensor([4, 0]), torch.tensor([5, 0])
+    pool = _pool(5, H, D, seed=42)
+    ref_pool = _clone_pool(pool)
+    out = torch.zeros(T * H, D, dtype=F64)
+    for off in (0, 4):
+        R.prepared_recurrent_ref(qn, kn, v, dec, beta, out, pool, idx, starts, tr_i, tr_l,
+                                 True, off, dtype=F64)
+    shp = (1, T, H, D)
+    ref = R.kda_recurrent(qn.reshape(shp), kn.reshape(shp), v.reshape(shp), g,
+                          beta.reshape(1, T, H), state_pool=ref_pool, state_indices=idx,
+                          cu_seqlens=starts, track_state_indices=tr_i, track_state_lens=tr_l,
+                          dtype=F64)
+    torch.testing.assert_close(out.reshape(shp), ref, rtol=1e-12, atol=1e-14)
+    torch.testing.assert_close(pool, ref_pool, rtol=1e-12, atol=1e-14)
+    assert not torch.equal(pool[4], _pool(5, H, D, seed=42)[4]), "tracked slot not written"
+
+
+def test_prepared_recurrent_ref_one_token_closed_form():
+    """One token from a zero state, decay 1: o = beta (qn . kn) v on the
+    launched heads only."""
+    H, D = 8, 8
+    qn, kn, v, _, beta, _ = _prepared_rec_inputs(1, H, D, seed=43)
+    dec = torch.ones(H, D, dtype=F64)
+    pool = torch.zeros(2, H, D, D, dtype=F64)
+    out = torch.zeros(H, D, dtype=F64)
+    R.prepared_recurrent_ref(qn, kn, v, dec, beta, out, pool, torch.tensor([1]),
+                             torch.tensor([0, 1]), head_offset=4, dtype=F64)
+    expect = beta[:, None] * (qn * kn).sum(-1, keepdim=True) * v
+    torch.testing.assert_close(out[4:], expect[4:], rtol=1e-12, atol=1e-14)
+    assert torch.equal(out[:4], torch.zeros(4, D, dtype=F64))
+
+
+def test_prepared_recurrent_ref_writes_only_its_rows_and_heads():
+    """Rows outside [starts[0], starts[N]) and heads outside the launch keep
+    the caller's values in ``out`` and in the pool (prepared_recurrent.cpp
+    writes rows [bos, eos) of its four heads only)."""
+    T, H, D = 12, 8, 8
+    qn, kn, v, dec, beta, _ = _prepared_rec_inputs(T, H, D, seed=44)
+    pool = _pool(3, H, D, seed=45)
+    before = _clone_pool(pool)
+    out = torch.full((T * H, D), 7.0, dtype=F64)
+    R.prepared_recurrent_ref(qn, kn, v, dec, beta, out, pool, torch.tensor([1]),
+                             torch.tensor([3, T - 2]), head_offset=4, dtype=F64)
+    o = out.reshape(T, H, D)
+    assert torch.equal(o[:3], torch.full_like(o[:3], 7.0))
+    assert torch.equal(o[T - 2:], torch.full_like(o[T - 2:], 7.0))
+    assert torch.equal(o[:, :4], torch.full_like(o[:, :4], 7.0))
+    assert not torch.equal(o[3:T - 2, 4:], torch.full_like(o[3:T - 2, 4:], 7.0))
+    assert torch.equal(pool[:, :4], before[:, :4])
+    assert torch.equal(pool[0], before[0]) and torch.equal(pool[2], before[2])
+    assert not torch.equal(pool[1, 4:], before[1, 4:])

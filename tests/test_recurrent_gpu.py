@@ -218,8 +218,14 @@ def test_config1_golden_fixture(gpu_ops):
 
 
 def test_config2_decode_b256(gpu_ops):
-    """256 sequences x 1 token, H=32, D=128, 512-slot pool."""
+    """256 sequences x 1 token, H=32, D=128, 512-slot pool.
+
+    The seeded permutation (seed 2) happens to miss slot 0, so its first entry
+    is replaced by the padding slot: one sequence then starts from a zero
+    state and must not write back, and slot 0 stays byte-identical."""
     perm = torch.randperm(512, generator=C.gen(2))[:256].tolist()
+    if 0 not in perm:
+        perm[0] = 0
     case = C.prepared_case(32, (1,) * 256, slots=512, indices=perm, seed=2)
     out, pool = _run_prepared(gpu_ops, case)
     ref_pool = C.clone_pool(case.pool)
@@ -287,13 +293,48 @@ def test_prepared_recurrent_decay_form(gpu_ops, k_contiguous):
     torch.cuda.synchronize()
     ref_pool = C.clone_pool(pool_k)
     ref_out = torch.zeros(T * H, D, dtype=torch.float32)
-    R.prepared_recurrent_ref(qn, kn, v, gdecay, beta, ref_out, ref_pool, torch.tensor([2]),
-                             torch.tensor([0, T]))
+    for off in (0, 4):
+        R.prepared_recurrent_ref(qn, kn, v, gdecay, beta, ref_out, ref_pool, torch.tensor([2]),
+                                 torch.tensor([0, T]), head_offset=off)
     C.assert_out(out.cpu(), ref_out, C.OUT_TOL, "out")
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "state")
     # The first launch touched heads 0-3 only.
     assert torch.equal(half[2, 4:], pool_k[2, 4:])
     assert not torch.equal(half[2, :4], pool_k[2, :4])
+
+
+def test_prepared_recurrent_writes_only_covered_rows(gpu_ops):
+    """A caller-owned ``out`` keeps every row its requests do not cover and
+    every head outside the launch (the reference's prepared kernels write rows
+    [bos, eos) of their four heads only): starts=[3, T-2], sentinel fill."""
+    H, D, T = 8, 128, 14
+    g_ = C.gen(15)
+    qn = R.l2norm_last(torch.randn(T * H, D, generator=g_)) * D ** -0.5
+    kn = R.l2norm_last(torch.randn(T * H, D, generator=g_))
+    v = torch.randn(T * H, D, generator=g_).bfloat16()
+    gdecay = torch.exp(torch.nn.functional.logsigmoid(torch.randn(T * H, D, generator=g_)))
+    beta = torch.sigmoid(torch.randn(T * H, generator=g_))
+    pool_k = C.native_pool(3, H, D, seed=16)
+    pool = C.to_dev(pool_k, DEV)
+    out = torch.full((T * H, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    starts = torch.tensor([3, T - 2], dtype=torch.int32)
+    gpu_ops.prepared_recurrent(qn.to(DEV), kn.to(DEV), v.to(DEV), gdecay.to(DEV), beta.to(DEV),
+                               out, pool, torch.tensor([1], dtype=torch.int32, device=DEV),
+                               starts.to(DEV), None, None, False, 4)
+    torch.cuda.synchronize()
+    ref_pool = C.clone_pool(pool_k)
+    ref_out = torch.full((T * H, D), 7.0, dtype=torch.float32)
+    R.prepared_recurrent_ref(qn, kn, v, gdecay, beta, ref_out, ref_pool, torch.tensor([1]),
+                             starts, head_offset=4)
+    got = out.cpu().float().reshape(T, H, D)
+    exp = ref_out.reshape(T, H, D)
+    sentinel = torch.full_like(got[:3], 7.0)
+    assert torch.equal(got[:3], sentinel), "rows before starts[0] were written"
+    assert torch.equal(got[T - 2:], torch.full_like(got[T - 2:], 7.0)), "rows past starts[N] written"
+    assert torch.equal(got[:, :4], torch.full_like(got[:, :4], 7.0)), "heads outside the launch written"
+    C.assert_out(out.cpu().reshape(T, H, D)[3:T - 2, 4:], exp[3:T - 2, 4:], C.OUT_TOL, "covered rows")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "state")
+    assert torch.equal(pool.cpu()[:, :4], pool_k[:, :4])
 
 
 # --- the C ABI on its own ------------------------------------------------------
@@ -456,6 +497,7 @@ def test_config5_decode_full_size(gpu_ops):
     before = {s: pool[int(perm[s])].cpu().clone() for s in sample}
     untouched = torch.ones(slots, dtype=torch.bool)
     untouched[perm] = False
+    untouched[0] = True  # the padding slot is read as zero and never written
     untouched_idx = untouched.nonzero().flatten().to(dev)
     untouched_before = pool.index_select(0, untouched_idx).clone()
 
@@ -468,15 +510,19 @@ def test_config5_decode_full_size(gpu_ops):
     for s in sample:
         rows = slice(s * steps, (s + 1) * steps)
         ref_pool = torch.zeros(2, heads, D, D)
-        ref_pool[1] = before[s]  # the sequence's own slot as slot 1
+        if int(perm[s]) > 0:
+            ref_pool[1] = before[s]  # the sequence's own slot as slot 1
         ref = R.kda_recurrent(q[:, rows].float().cpu() * D ** -0.5, k[:, rows].float().cpu(),
                               v[:, rows].float().cpu(), g[:, rows].cpu(), beta[:, rows].cpu(),
-                              state_pool=ref_pool, state_indices=torch.tensor([1], dtype=torch.int32),
+                              state_pool=ref_pool,
+                              state_indices=torch.tensor([1 if int(perm[s]) > 0 else 0],
+                                                         dtype=torch.int32),
                               cu_seqlens=torch.tensor([0, steps], dtype=torch.int32),
                               out_dtype=torch.float32)
         e_o = max(e_o, C.assert_out(out[:, rows].cpu(), ref, C.OUT_TOL, f"sequence {s} output"))
-        e_s = max(e_s, C.assert_rel(pool[int(perm[s])].cpu(), ref_pool[1], C.STATE_TOL,
-                                    f"sequence {s} state"))
+        if int(perm[s]) > 0:
+            e_s = max(e_s, C.assert_rel(pool[int(perm[s])].cpu(), ref_pool[1], C.STATE_TOL,
+                                        f"sequence {s} state"))
     print(f"config5 decode: output err {e_o:.2e}, state err {e_s:.2e}")
 
 
