@@ -18,8 +18,10 @@
 //                           chunk grid is sized on the host from T and N alone;
 //   K1 chunk_prepare_kernel one workgroup per (chunk, head), all chunks in
 //                           parallel: cumsum, Akk / Aqk on MFMA with exponents
-//                           anchored at each 16-row block start (all off-diagonal
-//                           factors e^(<=0)), the blocked triangular inverse in
+//                           anchored at each 16-row block's midpoint row (no
+//                           factor spans more than 8 tokens of decay, all
+//                           column factors of earlier blocks e^(<=0)), the
+//                           blocked triangular inverse in
 //                           fp32, w and u on MFMA; writes the scan's operands as
 //                           ready MFMA fragments;
 //   K2 chunk_scan_kernel    one workgroup per (sequence, head, 16 or 32 value
@@ -306,6 +308,11 @@ constexpr int kPadT = 144;  // bf16 row stride of tiles read transposed
 constexpr int kPadX = 68;   // fp32 row stride of [64][64] tiles (16-B rows)
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Akk / Aqk exponent anchor: row 7 of each 16-row block, and the largest
+// exponent (log2 units) a factor may take before it is clamped.
+constexpr int kAnchorRow = 7;
+constexpr float kMaxExp2 = 126.f;
 
 // All-ones if `keep`, else zero, opaque to the optimizer: a value masked with
 // it is used unconditionally, so its load cannot be sunk into a branch (a
@@ -636,11 +643,17 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         if (norm) {
             qscale = a.scale / sqrtf(sm.u.early.qss[0][ri] + sm.u.early.qss[1][ri] + 1e-6f);
         }
-        // the block's anchor row G[16I][.]
+        // The block's anchor row G[16I + 7][.]: a row factor e^(G_i - anchor)
+        // of the block spans at most 7 tokens of decay above 1, a column
+        // factor e^(anchor - G_j) at most 8 (diagonal block, j > anchor) and
+        // is e^(<=0) for every earlier block, so fp32 and bf16 hold both while
+        // 8 consecutive tokens decay by less than 2^kMaxExp2 (about 87 nat).
+        // Beyond that the exponents are clamped: results stay finite but are
+        // no longer exact (the precondition stated with the C ABI).
         float anc[2][8];
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
-            load_g8(16 * I, 2 * sh + sl, anc[sl]);
+            load_g8(16 * I + kAnchorRow, 2 * sh + sl, anc[sl]);
         }
         const float rki = sm.rnk[ri];
         bf16x8 Rh[2], Qh[2], Ql[2];
@@ -652,7 +665,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             load_g8(ri, s, gg);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float ex = ex2(gg[e] - anc[sl][e]);
+                const float ex = ex2(fminf(gg[e] - anc[sl][e], kMaxExp2));
                 const float qn = qv[sl][e] * qscale;
                 rv[e] = kk[e] * rki * ex;
                 qa[e] = qn * ex;
@@ -680,7 +693,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 load_g8(rj, s, gg);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    cv[e] = kk[e] * rkj * ex2(anc[sl][e] - gg[e]);
+                    cv[e] = kk[e] * rkj * ex2(fminf(anc[sl][e] - gg[e], kMaxExp2));
                 }
                 bf16x8 Ch, Cl;
                 split_bf16x8(cv, Ch, Cl);

@@ -176,7 +176,15 @@ typedef struct KdaChunkArgs {
 size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
                                  int32_t num_heads, int32_t head_dim);
 
-/* Chunked (chunk = 64 tokens) KDA over packed varlen sequences. `workspace`
+/* Chunked (chunk = 64 tokens) KDA over packed varlen sequences.
+ * Decay precondition: the intra-chunk products factor e^(G_i - G_j) as
+ * e^(G_i - a) e^(a - G_j) with the anchor a at the middle of each 16-token
+ * block, so no factor spans more than 8 tokens of decay. Results are exact
+ * (to the tolerance contract) while any 8 consecutive tokens of a channel
+ * decay by less than 2^126 (about 87 nat): always on the RAW path with
+ * lower_bound >= -10.9, and for LOG gates g >= -10.9 per token. Beyond it
+ * the exponents are clamped: outputs and states stay finite but inexact.
+ * `workspace`
  * must hold kda_chunk_workspace_bytes(...) bytes of device memory, 256-byte
  * aligned; its contents need no initialization. A single long sequence on few
  * heads forks its second segment's preparation onto a library-owned stream

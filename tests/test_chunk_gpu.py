@@ -189,6 +189,53 @@ def test_prepared_chunk_extreme_magnitudes(gpu_ops, q_mul, v_mul, pool_mul):
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
 
 
+@pytest.mark.parametrize("label,gfun", [
+    ("constant -7", lambda shape, gen: torch.full(shape, -7.0)),
+    ("constant -10", lambda shape, gen: torch.full(shape, -10.0)),
+    ("logsigmoid(randn-7)",
+     lambda shape, gen: torch.nn.functional.logsigmoid(torch.randn(shape, generator=gen) - 7.0)),
+    ("mixed per channel",
+     lambda shape, gen: torch.where(torch.rand(shape, generator=gen) < 0.5,
+                                    torch.full(shape, -9.5),
+                                    torch.nn.functional.logsigmoid(torch.randn(shape, generator=gen)))),
+])
+def test_prepared_chunk_strong_decay(gpu_ops, label, gfun):
+    """Planted strong per-token decays: the factored Akk / Aqk exponentials
+    are anchored at each 16-row block's midpoint, so within a diagonal block a
+    factor spans at most 8 tokens of decay (80 nat at g = -10). Outputs and
+    states stay finite and match the fp64 oracle, which evaluates
+    exp(G_i - G_j) directly."""
+    import dataclasses
+
+    case = C.prepared_case(2, (200, 64, 37), slots=5, indices=[1, 3, 2], seed=43)
+    case = dataclasses.replace(case, g=gfun(tuple(case.g.shape), C.gen(44)).float())
+    dev = _prepared_dev(case)
+    pool = C.to_dev(case.pool, DEV)
+    out = _chunk_prepared(gpu_ops, case, pool, dev)
+    ref_pool = C.clone_pool(case.pool).double()
+    ref = R.kda_chunk(case.q.double() * case.scale, case.k.double(), case.v.double(),
+                      case.g.double(), case.beta.double(), state_pool=ref_pool,
+                      state_indices=case.indices, cu_seqlens=case.cu_seqlens,
+                      dtype=torch.float64, out_dtype=torch.float64)
+    assert torch.isfinite(out).all() and torch.isfinite(pool).all(), label
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, f"{label} output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, f"{label} pool")
+
+
+def test_prepared_chunk_beyond_envelope_stays_finite(gpu_ops):
+    """Per-token decays beyond the stated envelope (8 tokens at g = -20 span
+    160 nat) give finite outputs and states: the factor exponents are clamped
+    rather than overflowing to inf / NaN."""
+    import dataclasses
+
+    case = C.prepared_case(2, (128,), slots=2, indices=[1], seed=45)
+    case = dataclasses.replace(case, g=torch.full(tuple(case.g.shape), -20.0))
+    dev = _prepared_dev(case)
+    pool = C.to_dev(case.pool, DEV)
+    out = _chunk_prepared(gpu_ops, case, pool, dev)
+    assert torch.isfinite(out).all() and torch.isfinite(pool).all()
+
+
 def test_prepared_chunk_many_sequences(gpu_ops):
     """More sequences than the chunk-index kernel has threads (1500 > 1024, so
     each thread sums several sequences' chunk counts): short ragged and empty
