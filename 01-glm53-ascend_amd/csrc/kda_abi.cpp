@@ -9,6 +9,8 @@ extern "C" const char *kda_status_string(int status) {
         case KDA_ERR_UNSUPPORTED: return "unsupported shape, dtype or mode";
         case KDA_ERR_LAUNCH: return "HIP kernel launch failed";
         case KDA_ERR_WORKSPACE: return "workspace missing or too small";
+        case KDA_ERR_TOO_LARGE:
+            return "arguments need more scratch than kda_chunk_launch_noalloc's static buffer holds";
         default: return "unknown status";
     }
 }

@@ -1741,9 +1741,11 @@ extern "C" size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs
     return kda::chunk::layout(num_tokens, num_seqs, num_heads).total;
 }
 
-extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_t workspace_bytes,
-                                void *stream) {
-    using namespace kda::chunk;
+namespace kda {
+namespace chunk {
+
+// Argument checks shared by both chunk entry points (no device access).
+int check_args(const KdaChunkArgs *args) {
     if (args == nullptr) {
         return KDA_ERR_INVALID_ARGUMENT;
     }
@@ -1779,21 +1781,16 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
         !aligned(a.gate, a.gate_mode == KDA_GATE_RAW ? 8 : 16)) {
         return KDA_ERR_INVALID_ARGUMENT;
     }
+    return KDA_OK;
+}
+
+// Enqueues the chunk kernels on `st` with `ws` (checked by the caller) as the
+// workspace. `allow_split` permits the two-segment form (which uses the
+// library's side stream).
+int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, bool allow_split) {
     const Layout LY = layout(a.num_tokens, a.num_seqs, a.num_heads);
-    if (workspace == nullptr || workspace_bytes < LY.total || !aligned(workspace, 256)) {
-        return KDA_ERR_WORKSPACE;
-    }
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    char *ws = static_cast<char *>(workspace);
     KdaChunkArgs kargs = a;
     int *cs = reinterpret_cast<int *>(ws + LY.chunk_start);
-    if (a.num_seqs > 1) {  // one sequence needs no chunk index (K1 and K2 derive it)
-        void *params[] = {&kargs, &cs};
-        if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_index_kernel), dim3(1), dim3(1024),
-                            params, 0, st) != hipSuccess) {
-            return KDA_ERR_LAUNCH;
-        }
-    }
     const int nrec = max_chunks(a.num_tokens, a.num_seqs);
     const int64_t prep_blocks = static_cast<int64_t>(nrec) * a.num_heads;
     const int64_t pairs = static_cast<int64_t>(a.num_seqs) * a.num_heads;
@@ -1801,6 +1798,13 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     const int64_t blocks = scan_blocks(pairs, nt);
     if (prep_blocks > 0x7fffffff || blocks > 0x7fffffff) {
         return KDA_ERR_INVALID_ARGUMENT;
+    }
+    if (a.num_seqs > 1) {  // one sequence needs no chunk index (K1 and K2 derive it)
+        void *params[] = {&kargs, &cs};
+        if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_index_kernel), dim3(1), dim3(1024),
+                            params, 0, st) != hipSuccess) {
+            return KDA_ERR_LAUNCH;
+        }
     }
     const void *prep = a.gate_mode == KDA_GATE_RAW
                            ? reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_RAW>)
@@ -1820,21 +1824,96 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
                                dim3(kScanThreads), params, 0, st) == hipSuccess;
     };
     SideStream side;
-    const bool split = a.num_seqs == 1 && nt == 1 && a.num_tokens >= kSplitMinTokens &&
+    const bool split = allow_split && a.num_seqs == 1 && nt == 1 && a.num_tokens >= kSplitMinTokens &&
                        pairs * 8 * 2 <= device_cus(st) && side_stream(st, side);
-    if (!split) {
-        return launch_prep(0, st) && launch_scan(0) ? KDA_OK : KDA_ERR_LAUNCH;
+    if (split) {
+        // st:    K1(seg 1) -> fork -> K2(seg 1) -> [wait join] -> K2(seg 2)
+        // side:                [wait fork] -> K1(seg 2) -> join
+        // (the side stream starts after K1 of the first segment, so its K1 runs
+        // on the CUs the first scan leaves idle)
+        std::lock_guard<std::mutex> lock(*side.order);
+        if (!launch_prep(1, st) || hipEventRecord(side.fork, st) != hipSuccess ||
+            hipStreamWaitEvent(side.stream, side.fork, 0) != hipSuccess ||
+            !launch_prep(2, side.stream) || hipEventRecord(side.join, side.stream) != hipSuccess ||
+            !launch_scan(1) || hipStreamWaitEvent(st, side.join, 0) != hipSuccess || !launch_scan(2)) {
+            return KDA_ERR_LAUNCH;
+        }
+        return KDA_OK;
     }
-    // st:    K1(seg 1) -> fork -> K2(seg 1) -> [wait join] -> K2(seg 2)
-    // side:                [wait fork] -> K1(seg 2) -> join
-    // (the side stream starts after K1 of the first segment, so its K1 runs
-    // on the CUs the first scan leaves idle)
-    std::lock_guard<std::mutex> lock(*side.order);
-    if (!launch_prep(1, st) || hipEventRecord(side.fork, st) != hipSuccess ||
-        hipStreamWaitEvent(side.stream, side.fork, 0) != hipSuccess || !launch_prep(2, side.stream) ||
-        hipEventRecord(side.join, side.stream) != hipSuccess || !launch_scan(1) ||
-        hipStreamWaitEvent(st, side.join, 0) != hipSuccess || !launch_scan(2)) {
+    return launch_prep(0, st) && launch_scan(0) ? KDA_OK : KDA_ERR_LAUNCH;
+}
+
+// The no-allocation entry point's scratch: one array per device, held until
+// the process ends. Host code never uses the array's name as an address: the
+// device address is resolved once per device with hipGetSymbolAddress (that
+// device current) and kept here.
+static __device__ __align__(256) char scratch[KDA_NOALLOC_SCRATCH_BYTES];
+
+// The device address of `scratch` on the device `st` runs on, or null.
+char *scratch_address(hipStream_t st) {
+    static std::mutex mu;
+    static char *addr[64] = {};
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(st, &dev) != hipSuccess) {
+        (void)hipGetLastError();
+        if (hipGetDevice(&dev) != hipSuccess) {
+            return nullptr;
+        }
+    }
+    if (dev < 0 || dev >= 64) {
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess) {
+            return nullptr;
+        }
+        void *ptr = nullptr;
+        const bool ok = hipSetDevice(dev) == hipSuccess &&
+                        hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess && ptr != nullptr;
+        (void)hipSetDevice(cur);
+        if (!ok) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        addr[dev] = static_cast<char *>(ptr);
+    }
+    return addr[dev];
+}
+
+}  // namespace chunk
+}  // namespace kda
+
+extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_t workspace_bytes,
+                                void *stream) {
+    using namespace kda::chunk;
+    const int rc = check_args(args);
+    if (rc != KDA_OK || args->num_seqs == 0) {
+        return rc;
+    }
+    const KdaChunkArgs &a = *args;
+    const Layout LY = layout(a.num_tokens, a.num_seqs, a.num_heads);
+    if (workspace == nullptr || workspace_bytes < LY.total || !aligned(workspace, 256)) {
+        return KDA_ERR_WORKSPACE;
+    }
+    return launch(a, static_cast<char *>(workspace), static_cast<hipStream_t>(stream), true);
+}
+
+extern "C" int kda_chunk_launch_noalloc(const KdaChunkArgs *args, void *stream) {
+    using namespace kda::chunk;
+    const int rc = check_args(args);
+    if (rc != KDA_OK || args->num_seqs == 0) {
+        return rc;
+    }
+    const KdaChunkArgs &a = *args;
+    if (layout(a.num_tokens, a.num_seqs, a.num_heads).total > KDA_NOALLOC_SCRATCH_BYTES) {
+        return KDA_ERR_TOO_LARGE;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char *ws = scratch_address(st);
+    if (ws == nullptr) {
         return KDA_ERR_LAUNCH;
     }
-    return KDA_OK;
+    return launch(a, ws, st, false);
 }

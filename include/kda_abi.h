@@ -57,7 +57,8 @@ typedef enum KdaStatus {
     KDA_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, misalignment */
     KDA_ERR_UNSUPPORTED = 2,      /* a shape / dtype / mode with no kernel */
     KDA_ERR_LAUNCH = 3,           /* the HIP runtime refused the launch */
-    KDA_ERR_WORKSPACE = 4         /* workspace missing or too small */
+    KDA_ERR_WORKSPACE = 4,        /* workspace missing or too small */
+    KDA_ERR_TOO_LARGE = 5         /* needs more scratch than kda_chunk_launch_noalloc holds */
 } KdaStatus;
 
 typedef enum KdaDType {
@@ -194,6 +195,24 @@ size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
  * multiples of 4 elements; q, k, v and out 8 bytes; gate 8 (RAW) or 16. */
 int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/* Bytes of the static device scratch behind kda_chunk_launch_noalloc. */
+#define KDA_NOALLOC_SCRATCH_BYTES (64u * 1024u * 1024u)
+
+/* kda_chunk_launch without a caller workspace and without any device
+ * allocation. No counterpart in the reference: for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The workspace is a static device array of
+ * KDA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; its address
+ * on a device is resolved on the first call on that device. Arguments whose
+ * kda_chunk_workspace_bytes exceed it return KDA_ERR_TOO_LARGE (at K = V =
+ * 128 roughly 600 (chunk, head) pairs, e.g. T = 1024 tokens on 32 heads, or
+ * T = 8192 on 4). Results are those of kda_chunk_launch on the same
+ * arguments, always in the single-pass form (no second stream). Every call on
+ * one GPU shares that GPU's array (its contents need no initialization, the
+ * last call's are left behind): calls that overlap on one GPU -- concurrent
+ * streams, or host threads -- race, and must be serialized by the caller. */
+int kda_chunk_launch_noalloc(const KdaChunkArgs *args, void *stream);
 
 /* Human-readable text of a KdaStatus. */
 const char *kda_status_string(int status);

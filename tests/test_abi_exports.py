@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     for expected in ("kda_recurrent_launch", "kda_chunk_launch", "kda_chunk_workspace_bytes",
-                     "kda_status_string", "kda_abi_version"):
+                     "kda_chunk_launch_noalloc", "kda_status_string", "kda_abi_version"):
         assert expected in names
 
 
@@ -121,3 +121,30 @@ def test_chunk_workspace_size_formula(lib):
         max_chunks = (T + 63) // 64 + N
         expected = header + rec * max_chunks * H + track * N * H + (65536 * H if N == 1 else 0)
         assert lib.kda_chunk_workspace_bytes(T, N, H, 128) == expected, (T, N, H)
+
+
+def test_noalloc_rejects_what_its_scratch_cannot_hold(lib):
+    """kda_chunk_launch_noalloc checks the arguments, then the size against its
+    static scratch, before any HIP call: a null block is invalid and a
+    prefill bigger than KDA_NOALLOC_SCRATCH_BYTES is refused with
+    KDA_ERR_TOO_LARGE (the addresses are never dereferenced)."""
+    lib.kda_chunk_launch_noalloc.restype = ctypes.c_int
+    lib.kda_chunk_launch_noalloc.argtypes = [ctypes.POINTER(_ChunkArgs), ctypes.c_void_p]
+    lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
+    lib.kda_chunk_workspace_bytes.argtypes = [ctypes.c_int32] * 4
+    lib.kda_status_string.restype = ctypes.c_char_p
+    lib.kda_status_string.argtypes = [ctypes.c_int]
+    limit = int(re.search(r"KDA_NOALLOC_SCRATCH_BYTES\s+\((\d+)u \* 1024u \* 1024u\)",
+                          open(HEADER).read()).group(1)) << 20
+    assert lib.kda_chunk_launch_noalloc(None, None) == 1
+    base = 1 << 20
+    T = 8192
+    assert lib.kda_chunk_workspace_bytes(T, 1, 32, 128) > limit
+    a = _ChunkArgs(q=base, k=base, v=base, gate=base, beta=base, state=base,
+                   state_stride_slot=32 * 128 * 128, state_stride_head=128 * 128, num_slots=4,
+                   state_indices=base, cu_seqlens=base, out=base, scale=1.0, num_seqs=1,
+                   num_tokens=T, num_heads=32, head_dim=128, qk_dtype=0, v_dtype=0, gate_mode=1)
+    assert lib.kda_chunk_launch_noalloc(ctypes.byref(a), None) == 5  # KDA_ERR_TOO_LARGE
+    assert b"noalloc" in lib.kda_status_string(5)
+    a.head_dim = 64
+    assert lib.kda_chunk_launch_noalloc(ctypes.byref(a), None) == 2  # unsupported, checked first
