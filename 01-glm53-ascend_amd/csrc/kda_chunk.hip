@@ -1686,6 +1686,9 @@ struct SideStream {
     std::mutex *order = nullptr;
 };
 
+// Returns false (the caller then runs the single-pass form) when the stream
+// of `main`'s device does not exist yet and `main` is being captured into a
+// graph: streams and events are never created during a capture.
 bool side_stream(hipStream_t main, SideStream &out) {
     static std::mutex mu;
     static std::mutex orders[64];
@@ -1703,6 +1706,11 @@ bool side_stream(hipStream_t main, SideStream &out) {
     std::lock_guard<std::mutex> lock(mu);
     SideStream &ss = streams[dev];
     if (ss.stream == nullptr) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(main, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+            (void)hipGetLastError();
+            return false;
+        }
         int cur = 0;
         if (hipGetDevice(&cur) != hipSuccess) {
             return false;
@@ -1830,15 +1838,20 @@ int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, bool allow_split) {
         // st:    K1(seg 1) -> fork -> K2(seg 1) -> [wait join] -> K2(seg 2)
         // side:                [wait fork] -> K1(seg 2) -> join
         // (the side stream starts after K1 of the first segment, so its K1 runs
-        // on the CUs the first scan leaves idle)
+        // on the CUs the first scan leaves idle). A side stream that another
+        // thread's graph capture has pulled in is not used.
         std::lock_guard<std::mutex> lock(*side.order);
-        if (!launch_prep(1, st) || hipEventRecord(side.fork, st) != hipSuccess ||
-            hipStreamWaitEvent(side.stream, side.fork, 0) != hipSuccess ||
-            !launch_prep(2, side.stream) || hipEventRecord(side.join, side.stream) != hipSuccess ||
-            !launch_scan(1) || hipStreamWaitEvent(st, side.join, 0) != hipSuccess || !launch_scan(2)) {
-            return KDA_ERR_LAUNCH;
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(side.stream, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
+            if (!launch_prep(1, st) || hipEventRecord(side.fork, st) != hipSuccess ||
+                hipStreamWaitEvent(side.stream, side.fork, 0) != hipSuccess ||
+                !launch_prep(2, side.stream) || hipEventRecord(side.join, side.stream) != hipSuccess ||
+                !launch_scan(1) || hipStreamWaitEvent(st, side.join, 0) != hipSuccess || !launch_scan(2)) {
+                return KDA_ERR_LAUNCH;
+            }
+            return KDA_OK;
         }
-        return KDA_OK;
+        (void)hipGetLastError();
     }
     return launch_prep(0, st) && launch_scan(0) ? KDA_OK : KDA_ERR_LAUNCH;
 }

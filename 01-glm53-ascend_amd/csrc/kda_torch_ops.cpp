@@ -149,6 +149,13 @@ PoolRef pool_ref(at::Tensor &pool) {
     return PoolRef{pool.data_ptr<float>(), pool.stride(0), pool.stride(1), pool.size(0)};
 }
 
+at::Tensor run_chunk(const char *op, KdaChunkArgs &args, const at::Tensor &q);
+
+// A prefill of K = V = 128 whose requests average at least this many tokens
+// runs in the chunked form (measured: 1024 tokens on 4 heads take ~1 ms
+// token by token, a few tens of microseconds in 64-token chunks).
+constexpr int64_t kChunkRouteTokensPerRequest = 128;
+
 // ---------------------------------------------------------------------------
 // kda_varlen_recurrent
 // ---------------------------------------------------------------------------
@@ -237,6 +244,44 @@ at::Tensor varlen_recurrent_impl(const char *op, const at::Tensor &A_log, const 
         return out.zero_();
     }
     const PoolRef pr = pool_ref(pool);
+
+    if (prefill && D == 128 && T >= kChunkRouteTokensPerRequest * N) {
+        // Long prefill: the chunked form of the same recurrence (64-token
+        // chunks on MFMA, within the tolerance contract of the token loop)
+        // instead of a serial pass over every token. Same slot, padding,
+        // tracking and uncovered-token rules.
+        KdaChunkArgs cargs{};
+        cargs.q = q.data_ptr();
+        cargs.k = k.data_ptr();
+        cargs.v = v.data_ptr();
+        cargs.gate = a.data_ptr();
+        cargs.beta = b.data_ptr();
+        cargs.A_log = A_log.data_ptr<float>();
+        cargs.dt_bias = dt_bias.data_ptr<float>();
+        cargs.state = pr.base;
+        cargs.state_stride_slot = pr.stride_slot;
+        cargs.state_stride_head = pr.stride_head;
+        cargs.num_slots = pr.num_slots;
+        cargs.state_indices = i32_ptr(idx32);
+        cargs.cu_seqlens = i32_ptr(cu32);
+        cargs.out = out.data_ptr();
+        if (ti32.has_value()) {
+            cargs.track_indices = i32_ptr(*ti32);
+            cargs.track_lens = i32_ptr(*tl32);
+        }
+        cargs.scale = static_cast<float>(scale);
+        cargs.lower_bound = static_cast<float>(lower_bound);
+        cargs.num_seqs = static_cast<int32_t>(N);
+        cargs.num_tokens = static_cast<int32_t>(T);
+        cargs.num_heads = static_cast<int32_t>(H);
+        cargs.head_dim = static_cast<int32_t>(D);
+        cargs.qk_dtype = KDA_BF16;
+        cargs.v_dtype = KDA_BF16;
+        cargs.gate_mode = KDA_GATE_RAW;
+        cargs.qk_l2norm = 1;
+        run_chunk(op, cargs, q);
+        return out;
+    }
 
     KdaRecurrentArgs args{};
     args.q = q.data_ptr();

@@ -186,3 +186,49 @@ def test_chunk_two_segment_graph_replay(gpu_ops):
         assert torch.equal(captured.cpu(), expected), f"replay {replay}: output"
         assert torch.equal(work.cpu(), ref_pool), f"replay {replay}: pool"
         assert expected.float().abs().sum() > 0
+
+
+_CAPTURE_FIRST = r"""
+import os, sys
+sys.path[:0] = [os.getcwd(), os.path.join(os.getcwd(), "01-glm53-ascend_amd")]
+import torch
+import sgl_glm53_ascend_ops  # noqa: F401
+from tests import kda_cases as C
+
+ops = torch.ops.sgl_glm53_ascend
+case = C.raw_case(1, (16384,), D=128, slots=3, indices=[1], seed=4242)
+pool = C.to_dev(case.pool, "cuda")
+init = pool.clone()
+kw = case.kwargs("cuda", pool=pool)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the first long call of the process
+    out = ops.kda_varlen_chunk(prefill=True, **kw)
+torch.cuda.synchronize()
+pool2 = C.to_dev(case.pool, "cuda")
+ref = ops.kda_varlen_chunk(prefill=True, **case.kwargs("cuda", pool=pool2))
+torch.cuda.synchronize()
+for replay in range(3):
+    pool.copy_(init)
+    junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), f"replay {replay}: output differs"
+    assert torch.equal(pool, pool2), f"replay {replay}: pool differs"
+print("CAPTURE-OK")
+"""
+
+
+def test_long_prefill_captured_before_any_eager_call(gpu_ops):
+    """A single long sequence eligible for the two-segment form, captured into
+    a graph as the process's first such call: the library has no side stream
+    yet and must not create one during a capture, so the captured call runs
+    the single-pass form. Runs in a fresh interpreter (this process has made
+    long calls already); every replay equals the eager result bitwise."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_FIRST], cwd=root, capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0 and "CAPTURE-OK" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
