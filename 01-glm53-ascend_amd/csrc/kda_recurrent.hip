@@ -232,6 +232,10 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     // Offset of this lane's vector j within a row of D elements.
     auto koff = [&](int j) { return 4 * kc + 4 * L * j; };
     const int64_t head_off = static_cast<int64_t>(head) * a.state_stride_head;
+    // A [K,V]-contiguous pool (state_v_contiguous, the prepared_recurrent
+    // layout of the reference) is read and written in place element by
+    // element: element (k, v) of a slot and head sits at k*D + v.
+    const bool vpool = a.state_v_contiguous != 0;
     float4 S[NP][EV];
     if (slot > 0) {
         const float *src = a.state + slot * a.state_stride_slot + head_off;
@@ -239,7 +243,12 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
         for (int p = 0; p < NP; ++p) {
 #pragma unroll
             for (int j = 0; j < EV; ++j) {
-                S[p][j] = load4_stream(src + static_cast<int64_t>(row0 + RS * p) * D + koff(j));
+                if (vpool) {
+                    const float *e = src + static_cast<int64_t>(koff(j)) * D + row0 + RS * p;
+                    S[p][j] = make_float4(e[0], e[D], e[2 * D], e[3 * D]);
+                } else {
+                    S[p][j] = load4_stream(src + static_cast<int64_t>(row0 + RS * p) * D + koff(j));
+                }
             }
         }
     } else {
@@ -267,17 +276,25 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     // State tiles are touched once per launch: streamed with nontemporal
     // loads and stores so they do not evict the token rows from the caches
     // (measured ~10% more HBM throughput than cached accesses).
-    auto store_state = [&](float *dst) {
+    auto store_state = [&](float *dst, bool vlayout) {
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
 #pragma unroll
             for (int j = 0; j < EV; ++j) {
-                store4_stream(dst + static_cast<int64_t>(row0 + RS * p) * D + koff(j), S[p][j]);
+                if (vlayout) {
+                    float *e = dst + static_cast<int64_t>(koff(j)) * D + row0 + RS * p;
+                    e[0] = S[p][j].x;
+                    e[D] = S[p][j].y;
+                    e[2 * D] = S[p][j].z;
+                    e[3 * D] = S[p][j].w;
+                } else {
+                    store4_stream(dst + static_cast<int64_t>(row0 + RS * p) * D + koff(j), S[p][j]);
+                }
             }
         }
     };
     if (track_slot > 0 && track_len == 0) {
-        store_state(a.state + track_slot * a.state_stride_slot + head_off);
+        store_state(a.state + track_slot * a.state_stride_slot + head_off, vpool);
     }
 
     // Per-head gate constants (RAW): exp(A_log[h]) and this lane's dt_bias.
@@ -432,10 +449,11 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
         const int step_i = t - bos;
         if (save_mid && step_i < a.mid_steps) {
             store_state(a.intermediate + n * a.mid_stride_req + step_i * a.mid_stride_step +
-                        static_cast<int64_t>(head) * a.mid_stride_head);
+                            static_cast<int64_t>(head) * a.mid_stride_head,
+                        false);
         }
         if (track_slot > 0 && step_i + 1 == track_len) {
-            store_state(a.state + track_slot * a.state_stride_slot + head_off);
+            store_state(a.state + track_slot * a.state_stride_slot + head_off, vpool);
         }
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
@@ -505,7 +523,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     }
 
     if (a.intermediate == nullptr && slot > 0) {
-        store_state(a.state + slot * a.state_stride_slot + head_off);
+        store_state(a.state + slot * a.state_stride_slot + head_off, vpool);
     }
 }
 

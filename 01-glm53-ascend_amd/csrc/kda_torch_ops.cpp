@@ -748,11 +748,15 @@ void prepared_recurrent(const at::Tensor &qn, const at::Tensor &kn, const at::Te
         return;
     }
     // The reference pool for this op is [K,V]-contiguous; the native pool of
-    // the other ops is K-contiguous. Both are accepted: the native one in
-    // place, the other through a K-contiguous working copy of the pool.
+    // the other ops is K-contiguous. Both are updated in place: the kernel
+    // reads and writes either layout (only the touched slots move).
     const bool k_contig = state.stride(2) == 1 && state.stride(3) == D;
-    at::Tensor work = k_contig ? state : state.transpose(-1, -2).contiguous().transpose(-1, -2);
-    const PoolRef pr = pool_ref(work);
+    const bool v_contig = state.stride(3) == 1 && state.stride(2) == D;
+    TORCH_CHECK(k_contig || v_contig, op,
+                ": state must be K-contiguous (stride(2)==1, stride(3)==D) or [K,V]-contiguous "
+                "(stride(3)==1, stride(2)==D), got strides (", state.stride(2), ", ", state.stride(3),
+                ")");
+    const PoolRef pr = pool_ref(state);
     const at::Tensor idx32 = as_int32(indices);
     const at::Tensor cu32 = as_int32(starts);
     std::optional<at::Tensor> ti32, tl32;
@@ -788,10 +792,8 @@ void prepared_recurrent(const at::Tensor &qn, const at::Tensor &kn, const at::Te
     args.v_dtype = v.scalar_type() == at::kFloat ? KDA_F32 : KDA_BF16;
     args.gate_mode = KDA_GATE_DECAY;
     args.qk_l2norm = 0;
+    args.state_v_contiguous = k_contig ? 0 : 1;
     check_ok(kda_recurrent_launch(&args, stream_of(qn)), op);
-    if (!k_contig) {
-        state.copy_(work);
-    }
 }
 
 }  // namespace

@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 1
+#define KDA_ABI_VERSION 2
 
 typedef enum KdaStatus {
     KDA_OK = 0,
@@ -128,6 +128,12 @@ typedef struct KdaRecurrentArgs {
     int32_t v_dtype;   /* KdaDType, also the output dtype */
     int32_t gate_mode; /* KdaGateMode */
     int32_t qk_l2norm; /* LOG mode: normalize q and k in the kernel */
+    /* State pool layout: 0 = K contiguous (the layout contract above); 1 =
+     * [K,V] contiguous, element (s, h, k, v) at
+     * state[s*state_stride_slot + h*state_stride_head + k*D + v] (the
+     * prepared_recurrent pool of the reference), read and written in place.
+     * Checkpoints (`intermediate`) are K contiguous either way. */
+    int32_t state_v_contiguous;
 } KdaRecurrentArgs;
 
 /* Fused recurrent (token-by-token) KDA over packed varlen sequences.

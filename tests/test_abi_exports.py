@@ -42,7 +42,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_version_and_status_text(lib):
     lib.kda_abi_version.restype = ctypes.c_int
-    assert lib.kda_abi_version() == 1
+    assert lib.kda_abi_version() == 2
     lib.kda_status_string.restype = ctypes.c_char_p
     lib.kda_status_string.argtypes = [ctypes.c_int]
     assert lib.kda_status_string(0) == b"ok"

@@ -301,6 +301,17 @@ def test_prepared_recurrent_decay_form(gpu_ops, k_contiguous):
     # The first launch touched heads 0-3 only.
     assert torch.equal(half[2, 4:], pool_k[2, 4:])
     assert not torch.equal(half[2, :4], pool_k[2, :4])
+    # Neither layout makes a pool-sized working copy: a pool of 256 slots
+    # (128 MiB) costs the call no more than its small index conversions.
+    big = (C.to_dev(C.native_pool(256, H, D, seed=15), DEV) if k_contiguous
+           else C.native_pool(256, H, D, seed=15).contiguous().to(DEV))
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    args[6] = big
+    gpu_ops.prepared_recurrent(*args, None, None, False, 0)
+    torch.cuda.synchronize()
+    assert torch.cuda.max_memory_allocated() - base < (1 << 20)
 
 
 def test_prepared_recurrent_writes_only_covered_rows(gpu_ops):
@@ -359,6 +370,7 @@ class _Args(ctypes.Structure):
         ("head_count", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("qk_dtype", ctypes.c_int32), ("v_dtype", ctypes.c_int32),
         ("gate_mode", ctypes.c_int32), ("qk_l2norm", ctypes.c_int32),
+        ("state_v_contiguous", ctypes.c_int32),
     ]
 
 
