@@ -97,7 +97,8 @@ def _torch_flags():
 
 
 def _atomic_link(cmd_without_output, dst, verbose):
-    fd, tmp = tempfile.mkstemp(prefix=os.path.basename(dst) + ".", suffix=".tmp", dir=PKG)
+    fd, tmp = tempfile.mkstemp(prefix=os.path.basename(dst) + ".", suffix=".tmp",
+                               dir=os.path.dirname(dst))
     os.close(fd)
     try:
         _run(cmd_without_output + ["-o", tmp], verbose)
@@ -107,8 +108,10 @@ def _atomic_link(cmd_without_output, dst, verbose):
             os.unlink(tmp)
 
 
-def build(verbose: bool = False) -> None:
-    os.makedirs(PKG, exist_ok=True)
+def build(verbose: bool = False, out_dir: str = PKG) -> None:
+    """Compile both libraries into ``out_dir`` (default: the package directory
+    in the source tree, where the loader finds them)."""
+    os.makedirs(out_dir, exist_ok=True)
     with tempfile.TemporaryDirectory(prefix="kda_build_") as obj_dir:
         procs = []
         objs = []
@@ -129,7 +132,7 @@ def build(verbose: bool = False) -> None:
                 raise RuntimeError(f"command failed ({p.returncode}): {' '.join(cmd)}\n{out}")
             if verbose and out.strip():
                 print(out, flush=True)
-        lib_abi = os.path.join(PKG, "libkda_amd.so")
+        lib_abi = os.path.join(out_dir, "libkda_amd.so")
         _atomic_link([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs], lib_abi, verbose)
 
         cflags, ldflags = _torch_flags()
@@ -139,9 +142,9 @@ def build(verbose: bool = False) -> None:
             _run(["g++", *cflags, f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj],
                  verbose)
             tobjs.append(obj)
-        lib_ops = os.path.join(PKG, "sgl_glm53_ascend_ops_lib.so")
+        lib_ops = os.path.join(out_dir, "sgl_glm53_ascend_ops_lib.so")
         _atomic_link(
-            ["g++", "-shared", "-fPIC", *tobjs, f"-L{PKG}", "-lkda_amd",
+            ["g++", "-shared", "-fPIC", *tobjs, f"-L{out_dir}", "-lkda_amd",
              "-Wl,-rpath,$ORIGIN", *ldflags],
             lib_ops,
             verbose,
