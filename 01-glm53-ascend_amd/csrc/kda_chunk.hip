@@ -27,17 +27,19 @@
 //   K2 chunk_scan_kernel    one workgroup per (sequence, head, 16 or 32 value
 //                           columns), the serial chunk recurrence: four chain
 //                           waves carry S (fp32, registers) and vnew, four
-//                           output waves compute o one phase behind; S and
-//                           vnew are exchanged through LDS.
+//                           output waves compute o one phase behind, four
+//                           loader waves stage the chain's operands in LDS;
+//                           S and vnew are exchanged through LDS.
 //
-// MFMA: v_mfma_f32_16x16x32_bf16 / _f16 with fp32 accumulation. Operands
-// whose rounding would break the tolerance contract are carried as bf16 hi +
-// lo pairs (x = hi + lo to ~2^-17) and multiplied in three passes
-// (hi*hi + hi*lo + lo*hi): u = T v (T split, v exact), Aqk, Aqk vnew and the
-// state update; Akk runs single-pass. w and q e^G are stored as fp16 (11-bit
-// significands, half the bytes of a bf16 pair) with a power-of-two scale per
-// fragment, and meet S as fp16 hi + lo (scaled per 32-row slice): w S single
-// pass, (q e^G) S two passes.
+// MFMA: v_mfma_f32_16x16x32_bf16 / _f16 with fp32 accumulation. Inside K1,
+// operands whose rounding would break the tolerance contract are carried as
+// bf16 hi + lo pairs (x = hi + lo to ~2^-17) and multiplied in two or three
+// passes: u = T v (T split, v exact) and Aqk (q split, then k split); Akk
+// runs single-pass. The record the scan reads holds every matrix operand as
+// fp16 (11-bit significands) with a power-of-two scale per fragment or row
+// tile: w, q e^G, kd^T and Aqk. The scan meets them with S_j as fp16 (scaled
+// per 32-row slice; S itself stays fp32) for w S and (q e^G) S, and with
+// vnew as fp16 hi + lo (~2^-22) for kd^T vnew and Aqk vnew.
 //
 // Fragment conventions (lane l, r = l % 16, g = l / 16), shared by A and B so
 // that C-layout accumulators can be fed back as B operands without moving
@@ -74,22 +76,32 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Workspace record of one (chunk, head), in 16-byte-per-lane fragments
 // (a fragment is 64 lanes x 16 B = 1 KiB).
 constexpr int kFrag = 1024;
+// Every matrix operand is fp16 with a power-of-two scale (held in the
+// scale block); the first 38 fragments are the chain's operands that every
+// column group of a (sequence, head) reads whole, in the order the scan
+// stages them.
 constexpr int kOffW = 0;                          // w fp16: A (mt 0..3, s 0..3)
-constexpr int kOffQg = kOffW + 16 * kFrag;        // q e^G fp16: A (mt, s)
-constexpr int kOffAqH = kOffQg + 16 * kFrag;      // Aqk hi: A (mt, s), see aq_frag
-constexpr int kOffAqL = kOffAqH + 6 * kFrag;      // Aqk lo
-constexpr int kOffKdH = kOffAqL + 6 * kFrag;      // kd^T hi: A (mk 0..7, s 0..1)
-constexpr int kOffKdL = kOffKdH + 16 * kFrag;     // kd^T lo
-constexpr int kOffU = kOffKdL + 16 * kFrag;       // u fp32: C (mt 0..3, vt 0..7)
+constexpr int kOffKd = kOffW + 16 * kFrag;        // kd^T fp16: A (mk 0..7, s 0..1)
+constexpr int kOffAq = kOffKd + 16 * kFrag;       // Aqk fp16: A (mt, s), see aq_frag
+constexpr int kOffQg = kOffAq + 6 * kFrag;        // q e^G fp16: A (mt, s)
+constexpr int kOffU = kOffQg + 16 * kFrag;        // u fp32: C (mt 0..3, vt 0..7)
 constexpr int kOffGl = kOffU + 32 * kFrag;        // e^(G_last) fp32 [128]
-constexpr int kOffSc = kOffGl + DK * 4;           // fp32 [32]: 2^-shift of w (mt*4+s), q e^G (16+mt*4+s)
-constexpr int kRecBytes = kOffSc + 256;           // 111360
+constexpr int kOffSc = kOffGl + DK * 4;           // fp32 scale block [128], indices below
+constexpr int kRecBytes = kOffSc + 512;           // 89088
+// Scale block: 2^-shift of each fp16 fragment group, and the two bounds the
+// scan derives vnew's scale from.
+constexpr int kScW = 0;      // [16] w fragment (mt, s): mt * 4 + s
+constexpr int kScQg = 16;    // [16] q e^G fragment (mt, s)
+constexpr int kScKd = 32;    // [8]  kd^T row tile mk (both token slices)
+constexpr int kScAq = 40;    // [4]  Aqk row tile mt (both token slices)
+constexpr int kScUmax = 44;  // [32] max |u| over row tile mt, column tile vt: mt * 8 + vt
+constexpr int kScWl1 = 76;   // [4]  max over the rows of tile mt of sum_k |w[t][k]|
 // Track record of one (sequence, head): operands of the state after r < len
 // tokens of the chunk holding the tracked position.
-constexpr int kTrOffKdH = 0;
-constexpr int kTrOffKdL = kTrOffKdH + 16 * kFrag;
-constexpr int kTrOffGl = kTrOffKdL + 16 * kFrag;
-constexpr int kTrBytes = kTrOffGl + DK * 4;       // 33280
+constexpr int kTrOffKd = 0;                       // fp16, scaled per row tile mk
+constexpr int kTrOffGl = kTrOffKd + 16 * kFrag;
+constexpr int kTrOffSc = kTrOffGl + DK * 4;       // fp32 [8]
+constexpr int kTrBytes = kTrOffSc + 256;          // 17152
 static_assert(kRecBytes % 256 == 0 && kTrBytes % 256 == 0, "records stay 256-B aligned");
 
 struct Layout {
@@ -212,19 +224,36 @@ __device__ __forceinline__ float wave_max(float x) {
     return fmaxf(a, b);
 }
 
-// One wave stores a whole fp16 fragment and its inverse scale.
-__device__ __forceinline__ void store_frag_f16(char *rec, int off, int idx, int sc_idx, int lane,
-                                               const float x[8]) {
+// One wave stores NF (1 or 2) consecutive fp16 fragments with one shared
+// scale, and writes the inverse scale to *sc.
+template <int NF>
+__device__ __forceinline__ void store_frags_f16(char *base, int off, int idx, float *sc, int lane,
+                                                const float (&x)[NF][8]) {
     float m = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        m = fmaxf(m, fabsf(x[e]));
+    for (int f = 0; f < NF; ++f) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            m = fmaxf(m, fabsf(x[f][e]));
+        }
     }
     const int sh = f16_shift(wave_max(m));
-    reinterpret_cast<u32x4 *>(rec + off)[idx * 64 + lane] = as_u32x4(to_f16x8(x, sh));
-    if (lane == 0) {
-        reinterpret_cast<float *>(rec + kOffSc)[sc_idx] = ldexpf(1.f, -sh);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        reinterpret_cast<u32x4 *>(base + off)[(idx + f) * 64 + lane] = as_u32x4(to_f16x8(x[f], sh));
     }
+    if (lane == 0) {
+        *sc = ldexpf(1.f, -sh);
+    }
+}
+__device__ __forceinline__ void store_frag_f16(char *rec, int off, int idx, int sc_idx, int lane,
+                                               const float x[8]) {
+    float y[1][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        y[0][e] = x[e];
+    }
+    store_frags_f16<1>(rec, off, idx, reinterpret_cast<float *>(rec + kOffSc) + sc_idx, lane, y);
 }
 
 __device__ __forceinline__ void store_frag(char *base, int off, int idx, int lane, bf16x8 v) {
@@ -673,7 +702,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             }
             Rh[sl] = to_bf16x8(rv);
             split_bf16x8(qa, Qh[sl], Ql[sl]);
-            store_frag_f16(rec, kOffQg, I * 4 + s, 16 + I * 4 + s, lane, qg);
+            store_frag_f16(rec, kOffQg, I * 4 + s, kScQg + I * 4 + s, lane, qg);
         }
         // pairs (I, J), J <= I, over this half's channels
 #pragma unroll
@@ -714,19 +743,16 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         const int mk = 2 * wave + tt;
         const int k = 16 * mk + r;
         const float gl = sm.u.early.G[BT - 1][k];
+        float x[2][8];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            float x[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int t = 32 * s + kperm(gq, e);
-                x[e] = kval(t, k) * ex2(gl - sm.u.early.G[t][k]);
+                x[s][e] = kval(t, k) * ex2(gl - sm.u.early.G[t][k]);
             }
-            bf16x8 fh, fl;
-            split_bf16x8(x, fh, fl);
-            store_frag(rec, kOffKdH, mk * 2 + s, lane, fh);
-            store_frag(rec, kOffKdL, mk * 2 + s, lane, fl);
         }
+        store_frags_f16<2>(rec, kOffKd, mk * 2, reinterpret_cast<float *>(rec + kOffSc) + kScKd + mk, lane, x);
     }
     if (tid < DK) {
         reinterpret_cast<float *>(rec + kOffGl)[tid] = ex2(sm.u.early.G[BT - 1][tid]);
@@ -744,19 +770,16 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 const int mk = 2 * wave + tt;
                 const int k = 16 * mk + r;
                 const float gr = sm.u.early.G[rr - 1][k];
+                float x[2][8];
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    float x[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int t = 32 * s + kperm(gq, e);
-                        x[e] = t < rr ? kval(t, k) * ex2(gr - sm.u.early.G[t][k]) : 0.f;
+                        x[s][e] = t < rr ? kval(t, k) * ex2(gr - sm.u.early.G[t][k]) : 0.f;
                     }
-                    bf16x8 fh, fl;
-                    split_bf16x8(x, fh, fl);
-                    store_frag(tr, kTrOffKdH, mk * 2 + s, lane, fh);
-                    store_frag(tr, kTrOffKdL, mk * 2 + s, lane, fl);
                 }
+                store_frags_f16<2>(tr, kTrOffKd, mk * 2, reinterpret_cast<float *>(tr + kTrOffSc) + mk, lane, x);
             }
             if (tid < DK) {
                 reinterpret_cast<float *>(tr + kTrOffGl)[tid] = ex2(sm.u.early.G[rr - 1][tid]);
@@ -872,24 +895,30 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     lds_barrier();
     {
         // Aqk fragments (mt = wave, s): rows 16 wave + r, zero above the diagonal
+        // (rows < 32 meet only slice 0; fragments aq_frag(wave, 0..1) are
+        // consecutive), one scale per row tile
         const int row = 16 * wave + r;
+        float x[2][8];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            if (s == 1 && wave < 2) {
-                break;  // an all-zero fragment (uniform per wave)
-            }
             const float4 x0 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 4 * gq]);
             const float4 x1 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 16 + 4 * gq]);
             const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            float x[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                x[e] = 32 * s + kperm(gq, e) <= row ? xv[e] : 0.f;
+                x[s][e] = 32 * s + kperm(gq, e) <= row ? xv[e] : 0.f;
             }
-            bf16x8 fh, fl;
-            split_bf16x8(x, fh, fl);
-            store_frag(rec, kOffAqH, aq_frag(wave, s), lane, fh);
-            store_frag(rec, kOffAqL, aq_frag(wave, s), lane, fl);
+        }
+        float *asc = reinterpret_cast<float *>(rec + kOffSc) + kScAq + wave;
+        if (wave < 2) {
+            float x1[1][8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x1[0][e] = x[0][e];
+            }
+            store_frags_f16<1>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x1);
+        } else {
+            store_frags_f16<2>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x);
         }
     }
 
@@ -1013,8 +1042,15 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 acc = mfma(Tl[s], vb, acc);
             }
             reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = acc;
+            const float um = wave_max(fmaxf(fmaxf(fabsf(acc[0]), fabsf(acc[1])),
+                                            fmaxf(fabsf(acc[2]), fabsf(acc[3]))));
+            if (lane == 0) {
+                reinterpret_cast<float *>(rec + kOffSc)[kScUmax + wave * 8 + vt] = um;
+            }
         }
-        // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k (K = token), B = T^T
+        // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k (K = token), B = T^T;
+        // wl1 sums |w| over this lane's columns of row 16 wave + r
+        float wl1 = 0.f;
 #pragma unroll
         for (int sp = 0; sp < 4; ++sp) {
             float x[8];
@@ -1034,9 +1070,17 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     x[4 * half + i] = acc[i];
+                    wl1 += fabsf(acc[i]);
                 }
             }
-            store_frag_f16(rec, kOffW, wave * 4 + sp, wave * 4 + sp, lane, x);
+            store_frag_f16(rec, kOffW, wave * 4 + sp, kScW + wave * 4 + sp, lane, x);
+        }
+        // the row sums over all 128 columns (four lane groups), then their maximum
+        wl1 += __shfl_xor(wl1, 16);
+        wl1 += __shfl_xor(wl1, 32);
+        wl1 = wave_max(wl1);
+        if (lane == 0) {
+            reinterpret_cast<float *>(rec + kOffSc)[kScWl1 + wave] = wl1;
         }
     }
 }
@@ -1044,48 +1088,110 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 // ---------------------------------------------------------------------------
 // K2: the serial chunk scan per (sequence, head, CW = 16 NT value columns).
 //
-// Eight waves in two roles, so every SIMD holds two independent instruction
-// streams:
-//   chain waves 0-3  own S rows [32c, 32c+32) x CW columns (fp32, registers)
-//                    and run the recurrence: publish S_j, vnew_j = u - w S_j,
-//                    publish vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j;
-//   output waves 4-7 own token rows [16o, 16o+16) and compute
-//                    o_j = (q e^G) S_j + Aqk vnew_j one phase behind the chain.
-// Per chunk j there are two workgroup barriers: B1(j) after S_j is published,
-// B2(j) after vnew_j is published. S_j and vnew_j live in LDS buffers indexed
-// by j's parity. Output waves compute (q e^G) S_j between B2(j) and B1(j+1)
-// (while the chain runs its state update) and add Aqk vnew_j between B1(j+1)
-// and B2(j+1); buffer j&1 is rewritten only at chunk j+2, after both. With
-// NT = 1 the chain waves compute Aqk vnew_j themselves after their state
-// update (chain wave c for rows [16c, 16c+16)) and hand it over in LDS, so
-// the output waves stream only q e^G; one extra barrier after the last chunk
-// covers the last hand-over.
+// Twelve waves in three roles. Every wave meets the same two workgroup
+// barriers per chunk j: B1(j) after S_j is published, B2(j) after vnew_j is.
+//   chain waves 0-3   own S rows [32c, 32c+32) x CW columns (fp32, registers)
+//                     and run the recurrence: publish S_j, vnew_j = u - w S_j,
+//                     publish vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j,
+//                     then Aqk vnew_j for output rows [16c, 16c+16);
+//   output waves 4-7  own token rows [16o, 16o+16): (q e^G) S_j between B2(j)
+//                     and B1(j+1), then o_j = that + Aqk vnew_j and its store
+//                     between B1(j+1) and B2(j+1); they load their q e^G
+//                     fragments themselves, a chunk ahead;
+//   loader waves 8-11 copy the chain's operands of chunk j+1 (w, kd^T, Aqk,
+//                     this group's u, e^(G_last), the scales), loaded into
+//                     their registers after B2(j-2), into the LDS stage of
+//                     j+1's parity between B1(j) and B2(j) (every reader of
+//                     that stage's previous chunk j-1 finished before B1(j)),
+//                     then issue the loads of chunk j+3. The recurrence never
+//                     waits to issue a global load.
+// S_j, vnew_j, the Aqk hand-over and the stage are indexed by j's parity; a
+// buffer of parity j&1 is rewritten only after B1(j+1) or later, when its
+// chunk-j readers are done. One barrier B0 before the first chunk publishes
+// the first stage; one after the last chunk covers the last hand-over.
 //
-// The chunk operands (w, kd, q e^G, Aqk: ~80 KiB per chunk) are the same for
-// every column group of a (sequence, head), so a wider group (NT = 2) reads
-// fewer operand bytes per unit of work; a narrower one (NT = 1) has the
-// shorter serial step. The host picks NT from the number of chains.
+// S_j is published as fp16 scaled per 32-row slice (the state itself stays
+// fp32 in registers). vnew is exchanged as fp16 hi + lo scaled by 2^sv, where
+// 2^-sv bounds |vnew| <= max|u| + max_t sum_k |w[t][k]| max|S_j| (both maxima
+// from the record, max|S_j| from the publish) inside [2^13, 2^14): the pair
+// holds vnew to ~2^-22 of that bound and cannot overflow.
+//
+// The chunk operands (~42 KiB of w, kd^T and Aqk plus 16 KiB of q e^G) are
+// the same for every column group of a (sequence, head), so a wider group
+// (NT = 2) reads fewer operand bytes per unit of work; a narrower one
+// (NT = 1) has the shorter serial step. The host picks NT from the number of
+// chains.
 // ---------------------------------------------------------------------------
 
-constexpr int kScanThreads = 512;
+constexpr int kScanThreads = 768;
+constexpr int kStKd = 16;  // stage fragment indices: w at 0, kd^T, Aqk, then u
+constexpr int kStAq = 32;
+constexpr int kStU = 38;
+static_assert(kOffKd == kStKd * kFrag && kOffAq == kStAq * kFrag && kOffQg == kStU * kFrag &&
+                  kOffSc == kOffGl + DK * 4,
+              "the stage copies the record's first 38 fragments in order, then gl and the scale block");
+
+// Stage of one chunk for NT column tiles: 38 shared fragments, u (mt, ct) at
+// kStU + mt NT + ct, then e^(G_last) [128] and the scale block [128].
+template <int NT>
+struct Stage {
+    static constexpr int kFrags = kStU + 4 * NT + 1;
+    static constexpr int kMisc = (kStU + 4 * NT) * kFrag;
+    static constexpr int kLoadPer = (kFrags + 3) / 4;  // fragments per loader wave
+    // record offset of stage fragment f for column group vt
+    __device__ static int src(int f, int vt) {
+        if (f < kStU) {
+            return f * kFrag;
+        }
+        if (f < kStU + 4 * NT) {
+            const int u = f - kStU;
+            return kOffU + ((u / NT) * 8 + NT * vt + u % NT) * kFrag;
+        }
+        return kOffGl;
+    }
+};
+
+template <int NT>
+struct ScanShared {
+    char stg[2][Stage<NT>::kFrags * kFrag];  // chain operands by parity, fragments in lane order
+    u32x4 sbuf[2][4][NT][64];                // S_j as fp16 B fragments: [parity][slice][tile][lane]
+    u32x4 vbuf[2][2][2][NT][64];             // vnew_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
+    f32x4 obuf[2][4][NT][64];                // Aqk vnew_j rows [16c, 16c+16) from chain wave c
+    float sscale[2][4];                      // 2^-shift of each S_j slice in sbuf
+    float smax[2][4];                        // max |S_j| of each slice
+    uint32_t otile[4][16][8 * NT];           // per output wave: 16 rows x CW bf16 columns
+};
+static_assert(sizeof(ScanShared<2>) <= 160 * 1024, "the scan's LDS budget");
+
+__device__ __forceinline__ f16x8 stage_frag(const char *st, int f, int lane) {
+    return as_f16x8(reinterpret_cast<const u32x4 *>(st + f * kFrag)[lane]);
+}
+
+__device__ __forceinline__ uint32_t f16_bits2(_Float16 a, _Float16 b) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+// (x0, x1) * 2^sh = hi + lo as packed fp16 pairs
+__device__ __forceinline__ void split_f16x2(float x0, float x1, int sh, uint32_t &hi, uint32_t &lo) {
+    const float a0 = ldexpf(x0, sh);
+    const float a1 = ldexpf(x1, sh);
+    const _Float16 h0 = static_cast<_Float16>(a0);
+    const _Float16 h1 = static_cast<_Float16>(a1);
+    hi = f16_bits2(h0, h1);
+    lo = f16_bits2(static_cast<_Float16>(a0 - static_cast<float>(h0)),
+                   static_cast<_Float16>(a1 - static_cast<float>(h1)));
+}
 
 // SEG: the two-segment form (seg_arg 1 or 2); without it every launch scans
 // the whole sequence and the segment logic compiles away.
 template <int NT, bool SEG>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws,
                                                                   int seg_arg) {
+    using St = Stage<NT>;
     const int seg = SEG ? seg_arg : 0;
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
-    __shared__ u32x4 sbuf[2][4][2][NT][64];         // S_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
-    __shared__ float sscale[2][4];                  // 2^-shift of each S_j slice in sbuf
-    // Aqk vnew_j rows [16c, 16c+16) from chain wave c (NT = 1: the chain
-    // waves take that product so the output waves' operand stream is only
-    // q e^G)
-    constexpr bool kAqChain = NT == 1;
-    __shared__ f32x4 obuf[2][4][kAqChain ? NT : 1][64];
-    __shared__ uint32_t vbuf[2][2][2][NT][64][4];   // vnew_j as B fragments: [parity][slice][hi, lo][tile]
-    __shared__ uint32_t otile[4][16][CW / 2];       // per output wave: 16 rows x CW bf16 columns
+    __shared__ ScanShared<NT> sm;
 
     const int H = a.num_heads;
     const int N = a.num_seqs;
@@ -1117,8 +1223,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    // wave index as a scalar: the role branch below must be wave-uniform, since
-    // both roles meet at the same workgroup barriers
+    // wave index as a scalar: the role branches below must be wave-uniform,
+    // since every role meets the same workgroup barriers
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = w & 3;
     const int r = lane & 15;
@@ -1147,15 +1253,13 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
         }
         const int64_t head_off = static_cast<int64_t>(h) * a.state_stride_head;
-        // state element (row 16 kt + 4 gq + i, column col0 + 16 ct + r) of slot s
+        // S rows [32wr, 32wr+32): tiles (kt = 2wr + tt, ct), lane holds
+        // S[16kt + 4gq + i][col0 + 16ct + r]; the same element of slot s, and
+        // of the carry buffer between segments
         auto state_ptr = [&](int s, int tt, int ct) {
             return a.state + s * a.state_stride_slot + head_off +
                    static_cast<int64_t>(col0 + 16 * ct + r) * DK + 16 * (2 * wr + tt) + 4 * gq;
         };
-
-        // S rows [32wr, 32wr+32): tiles (kt = 2wr + tt, ct), lane holds
-        // S[16kt + 4gq + i][col0 + 16ct + r].
-        // the same element in the carry buffer between segments
         auto carry_ptr = [&](int tt, int ct) {
             return carry + static_cast<int64_t>(col0 + 16 * ct + r) * DK + 16 * (2 * wr + tt) + 4 * gq;
         };
@@ -1190,55 +1294,47 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         }
         const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
 
-        // One chunk's chain operands; two sets alternate so the next chunk's
-        // fragments are in flight while this chunk computes.
-        struct Ops {
+        // Operands of phase B (w, u and the scalars of vnew's scale) are read
+        // from the stage a chunk ahead, during the previous chunk's phase C
+        // (the stage of chunk j+1 is complete from B2(j)); those of phase C
+        // (kd^T, Aqk, e^(G_last)) during phase B.
+        struct OpsB {
             f16x8 Wf[4];
-            bf16x8 Kh[2][2], Kl[2][2];
-            bf16x8 Ah[2], Al[2];  // Aqk rows [16wr, 16wr+16) (kAqChain)
-            f32x4 u[NT], gl[2];
+            f32x4 uu[NT];
             float4 wsc;
+            float umax, wl1;
         };
-        auto load_ops = [&](Ops &op, int j) {
-            const char *rec = rec_of(j);
+        auto read_b = [&](OpsB &op, int j) {
+            const char *st = sm.stg[j & 1];
+            const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                op.Wf[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffW)[(wr * 4 + s) * 64 + lane]);
+                op.Wf[s] = stage_frag(st, wr * 4 + s, lane);
             }
-            op.wsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 16 * wr);
-            if constexpr (kAqChain) {
-                // rows [16wr, 16wr+16) meet columns >= 32 only for wr >= 2
-                op.Ah[0] = load_frag(rec, kOffAqH, aq_frag(wr, 0), lane);
-                op.Al[0] = load_frag(rec, kOffAqL, aq_frag(wr, 0), lane);
-                if (wr >= 2) {
-                    op.Ah[1] = load_frag(rec, kOffAqH, aq_frag(wr, 1), lane);
-                    op.Al[1] = load_frag(rec, kOffAqL, aq_frag(wr, 1), lane);
-                }
-            }
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-#pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    op.Kh[tt][s] = load_frag(rec, kOffKdH, (2 * wr + tt) * 2 + s, lane);
-                    op.Kl[tt][s] = load_frag(rec, kOffKdL, (2 * wr + tt) * 2 + s, lane);
-                }
-            }
+            float um = 0.f;
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                op.u[ct] = reinterpret_cast<const f32x4 *>(rec + kOffU)[(wr * 8 + NT * vt + ct) * 64 + lane];
-            }
+                op.uu[ct] = reinterpret_cast<const f32x4 *>(st + (kStU + wr * NT + ct) * kFrag)[lane];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                op.gl[tt] = *reinterpret_cast<const f32x4 *>(rec + kOffGl +
-                                                             4 * (16 * (2 * wr + tt) + 4 * gq));
+                for (int mt = 0; mt < 4; ++mt) {
+                    um = fmaxf(um, sc[kScUmax + mt * 8 + NT * vt + ct]);
+                }
             }
+            op.umax = um;
+            op.wsc = *reinterpret_cast<const float4 *>(sc + kScW + 4 * wr);
+            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScWl1);
+            op.wl1 = fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w));
         };
-
-        auto step = [&](const Ops &op, int j) {
+        auto step = [&](const OpsB &ob, OpsB &next, int j) {
             const int p = j & 1;
             const int len = eos - (bos + BT * j) < BT ? eos - (bos + BT * j) : BT;
-            // A. publish S_j (slice wr) as fp16 hi/lo B fragments, scaled by
-            // a power of two from the slice's largest magnitude
+            const char *st = sm.stg[p];
+            const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
+
+            // A. publish S_j (slice wr) as fp16 B fragments, scaled by a power
+            // of two from the slice's largest magnitude (the state itself stays
+            // fp32 in registers; only its products with w and q e^G use the
+            // rounded copy)
             {
                 float m = 0.f;
 #pragma unroll
@@ -1251,7 +1347,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                         }
                     }
                 }
-                const int ssh = f16_shift(wave_max(m));
+                m = wave_max(m);
+                const int ssh = f16_shift(m);
 #pragma unroll
                 for (int ct = 0; ct < NT; ++ct) {
                     float x[8];
@@ -1260,166 +1357,157 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                         x[i] = S[0][ct][i];
                         x[4 + i] = S[1][ct][i];
                     }
-                    f16x8 hi, lo;
-                    split_f16x8(x, ssh, hi, lo);
-                    sbuf[p][wr][0][ct][lane] = as_u32x4(hi);
-                    sbuf[p][wr][1][ct][lane] = as_u32x4(lo);
+                    sm.sbuf[p][wr][ct][lane] = as_u32x4(to_f16x8(x, ssh));
                 }
                 if (lane == 0) {
-                    sscale[p][wr] = ldexpf(1.f, -ssh);
+                    sm.sscale[p][wr] = ldexpf(1.f, -ssh);
+                    sm.smax[p][wr] = m;
                 }
             }
             lds_barrier();  // B1(j)
-            // B. vnew rows [16wr, 16wr+16) = u - w S_j (single pass, one
-            // product per slice, then scaled), published as bf16 hi/lo;
-            // tile mt = wr is half wr%2 of slice wr/2
-            const int sl = wr >> 1;
-            const int hf = (wr & 1) * 2;
-            float fw[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                fw[s] = op.wsc[s] * sscale[p][s];
-            }
+            // B. vnew rows [16wr, 16wr+16) = u - w S_j (one product per slice,
+            // then scaled), published as fp16 hi/lo scaled by 2^sv; tile wr is
+            // half wr%2 of slice wr/2. Phase C's operands of chunk j are read
+            // behind the first tile's S fragments.
+            const float4 sx = *reinterpret_cast<const float4 *>(&sm.smax[p][0]);
+            const float4 ss = *reinterpret_cast<const float4 *>(&sm.sscale[p][0]);
+            const int sv = f16_shift(ob.umax + ob.wl1 * fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
+            const float inv_v = ldexpf(1.f, -sv);
+            const float fw[4] = {ob.wsc.x * ss.x, ob.wsc.y * ss.y, ob.wsc.z * ss.z, ob.wsc.w * ss.w};
+            f16x8 Kd[2][2];
+            f16x8 Aq[2];
+            f32x4 gl[2];
+            float2 kdsc;
+            float aqsc;
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
                 f32x4 acc[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    acc[s] = mfma(op.Wf[s], as_f16x8(sbuf[p][s][0][ct][lane]), z4);
+                    acc[s] = mfma(ob.Wf[s], as_f16x8(sm.sbuf[p][s][ct][lane]), z4);
                 }
-                uint32_t hp[2], lp[2];
+                if (ct == 0) {
 #pragma unroll
-                for (int q2 = 0; q2 < 2; ++q2) {
-                    float ws0 = 0.f, ws1 = 0.f;
+                    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                        for (int s = 0; s < 2; ++s) {
+                            Kd[tt][s] = stage_frag(st, kStKd + (2 * wr + tt) * 2 + s, lane);
+                        }
+                    }
+                    // Aqk rows [16wr, 16wr+16) meet tokens >= 32 only for wr >= 2
+                    Aq[0] = stage_frag(st, kStAq + aq_frag(wr, 0), lane);
+                    Aq[1] = stage_frag(st, kStAq + aq_frag(wr, wr >= 2 ? 1 : 0), lane);
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        gl[tt] = reinterpret_cast<const f32x4 *>(st + St::kMisc)[4 * (2 * wr + tt) + gq];
+                    }
+                    kdsc = *reinterpret_cast<const float2 *>(sc + kScKd + 2 * wr);
+                    aqsc = sc[kScAq + wr];
+                }
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float x = 0.f;
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
-                        ws0 += fw[s] * acc[s][2 * q2];
-                        ws1 += fw[s] * acc[s][2 * q2 + 1];
+                        x += fw[s] * acc[s][i];
                     }
-                    const float v0 = op.u[ct][2 * q2] - ws0;
-                    const float v1 = op.u[ct][2 * q2 + 1] - ws1;
-                    hp[q2] = pack_bf16x2(v0, v1);
-                    lp[q2] = pack_bf16x2(v0 - __uint_as_float(hp[q2] << 16),
-                                         v1 - __uint_as_float(hp[q2] & 0xffff0000u));
+                    v[i] = ob.uu[ct][i] - x;
                 }
-                vbuf[p][sl][0][ct][lane][hf] = hp[0];
-                vbuf[p][sl][0][ct][lane][hf + 1] = hp[1];
-                vbuf[p][sl][1][ct][lane][hf] = lp[0];
-                vbuf[p][sl][1][ct][lane][hf + 1] = lp[1];
+                uint32_t hp[2], lp[2];
+                split_f16x2(v[0], v[1], sv, hp[0], lp[0]);
+                split_f16x2(v[2], v[3], sv, hp[1], lp[1]);
+                const int sl = wr >> 1;
+                const int hf = (wr & 1) * 2;
+                uint32_t *vh = reinterpret_cast<uint32_t *>(&sm.vbuf[p][sl][0][ct][lane]);
+                uint32_t *vl = reinterpret_cast<uint32_t *>(&sm.vbuf[p][sl][1][ct][lane]);
+                vh[hf] = hp[0];
+                vh[hf + 1] = hp[1];
+                vl[hf] = lp[0];
+                vl[hf + 1] = lp[1];
             }
             lds_barrier();  // B2(j)
-            // C. S_{j+1} = e^(G_last) S_j + kd^T vnew_j (3-pass)
-            auto vfrag = [&](int s, int hl, int ct) {
-                return as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][hl][ct][lane][0]));
-            };
-            // tracked prefix strictly inside this chunk
+            // C. S_{j+1} = e^(G_last) S_j + kd^T vnew_j (fp16 kd against vnew
+            // hi + lo, then both scales), one column tile at a time; the
+            // tracked prefix strictly inside this chunk is taken from S_j
+            // first. The next chunk's phase-B operands are read behind the
+            // first tile's vnew (clamped: at the last chunk this rereads the
+            // current stage, which no one rewrites before B1(j+2)).
             const int rr = track_len - BT * j;
-            if (track_slot > 0 && rr > 0 && rr < len) {
-                f32x4 St[2][NT];
+            const bool track_in = track_slot > 0 && rr > 0 && rr < len;
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    const f32x4 g2 = *reinterpret_cast<const f32x4 *>(
-                        tr + kTrOffGl + 4 * (16 * (2 * wr + tt) + 4 * gq));
-                    bf16x8 th[2], tl[2];
+            for (int ct = 0; ct < NT; ++ct) {
+                f16x8 vh[2], vl[2];
 #pragma unroll
-                    for (int s = 0; s < 2; ++s) {
-                        th[s] = load_frag(tr, kTrOffKdH, (2 * wr + tt) * 2 + s, lane);
-                        tl[s] = load_frag(tr, kTrOffKdL, (2 * wr + tt) * 2 + s, lane);
-                    }
+                for (int s = 0; s < 2; ++s) {
+                    vh[s] = as_f16x8(sm.vbuf[p][s][0][ct][lane]);
+                    vl[s] = as_f16x8(sm.vbuf[p][s][1][ct][lane]);
+                }
+                if (ct == 0) {
+                    read_b(next, j + 1 < j1 ? j + 1 : j);
+                }
+                if (track_in) {
+                    const float *tsc = reinterpret_cast<const float *>(tr + kTrOffSc);
 #pragma unroll
-                    for (int ct = 0; ct < NT; ++ct) {
+                    for (int tt = 0; tt < 2; ++tt) {
+                        const f32x4 g2 = *reinterpret_cast<const f32x4 *>(
+                            tr + kTrOffGl + 4 * (16 * (2 * wr + tt) + 4 * gq));
                         f32x4 tu = z4;
 #pragma unroll
                         for (int s = 0; s < 2; ++s) {
-                            const bf16x8 vh = vfrag(s, 0, ct);
-                            const bf16x8 vl = vfrag(s, 1, ct);
-                            tu = mfma(th[s], vh, tu);
-                            tu = mfma(th[s], vl, tu);
-                            tu = mfma(tl[s], vh, tu);
+                            const f16x8 th = as_f16x8(reinterpret_cast<const u32x4 *>(
+                                tr + kTrOffKd)[((2 * wr + tt) * 2 + s) * 64 + lane]);
+                            tu = mfma(th, vh[s], tu);
+                            tu = mfma(th, vl[s], tu);
                         }
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            St[tt][ct][i] = S[tt][ct][i] * g2[i] + tu[i];
-                        }
-                    }
-                }
-                store_S(track_slot, St);
-            }
-#pragma unroll
-            for (int ct = 0; ct < NT; ++ct) {
-                bf16x8 vh[2], vl[2];
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    vh[s] = vfrag(s, 0, ct);
-                    vl[s] = vfrag(s, 1, ct);
-                }
-                f32x4 su[2] = {z4, z4};
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        su[tt] = mfma(op.Kh[tt][s], vh[s], su[tt]);
-                    }
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        su[tt] = mfma(op.Kh[tt][s], vl[s], su[tt]);
-                    }
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        su[tt] = mfma(op.Kl[tt][s], vh[s], su[tt]);
+                        const float f = tsc[2 * wr + tt] * inv_v;
+                        *reinterpret_cast<float4 *>(state_ptr(track_slot, tt, ct)) =
+                            make_float4(S[tt][ct][0] * g2[0] + tu[0] * f, S[tt][ct][1] * g2[1] + tu[1] * f,
+                                        S[tt][ct][2] * g2[2] + tu[2] * f, S[tt][ct][3] * g2[3] + tu[3] * f);
                     }
                 }
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        S[tt][ct][i] = S[tt][ct][i] * op.gl[tt][i] + su[tt][i];
-                    }
-                }
-            }
-            if constexpr (kAqChain) {
-                // Aqk vnew_j rows [16wr, 16wr+16) (3-pass), for output wave wr
-#pragma unroll
-                for (int ct = 0; ct < NT; ++ct) {
-                    f32x4 acc = z4;
+                    f32x4 su = z4;
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
-                        if (s == 1 && wr < 2) {
-                            break;  // Aqk is zero there (uniform per wave)
-                        }
-                        const bf16x8 vh = vfrag(s, 0, ct);
-                        const bf16x8 vl = vfrag(s, 1, ct);
-                        acc = mfma(op.Ah[s], vh, acc);
-                        acc = mfma(op.Ah[s], vl, acc);
-                        acc = mfma(op.Al[s], vh, acc);
+                        su = mfma(Kd[tt][s], vh[s], su);
+                        su = mfma(Kd[tt][s], vl[s], su);
                     }
-                    obuf[p][wr][ct][lane] = acc;
+                    const float f = (tt == 0 ? kdsc.x : kdsc.y) * inv_v;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        S[tt][ct][i] = S[tt][ct][i] * gl[tt][i] + su[i] * f;
+                    }
                 }
+                // Aqk vnew_j rows [16wr, 16wr+16), for output wave wr
+                f32x4 acc2 = mfma(Aq[0], vh[0], z4);
+                acc2 = mfma(Aq[0], vl[0], acc2);
+                if (wr >= 2) {
+                    acc2 = mfma(Aq[1], vh[1], acc2);
+                    acc2 = mfma(Aq[1], vl[1], acc2);
+                }
+                sm.obuf[p][wr][ct][lane] = acc2 * (aqsc * inv_v);
             }
             if (track_slot > 0 && rr == len) {
                 store_S(track_slot, S);
             }
         };
 
-        // The prefetches are unconditional (clamped to the last chunk) so the
-        // compiler's wait counts stay exact on every path through the loop.
-        Ops opA, opB;
+        lds_barrier();  // B0: the first chunk's stage is written
+        OpsB obA, obB;
         if (j1 > j0) {
-            load_ops(opA, j0);
+            read_b(obA, j0);
         }
         for (int j = j0; j < j1; j += 2) {
-            load_ops(opB, j + 1 < j1 ? j + 1 : j1 - 1);
-            step(opA, j);
+            step(obA, obB, j);
             if (j + 1 >= j1) {
                 break;
             }
-            load_ops(opA, j + 2 < j1 ? j + 2 : j1 - 1);
-            step(opB, j + 1);
+            step(obB, obA, j + 1);
         }
-        if constexpr (kAqChain) {
-            if (j1 > j0) {
-                lds_barrier();  // B1(j1), matched by the output waves' last finish
-            }
+        if (j1 > j0) {
+            lds_barrier();  // B1(j1): the last Aqk vnew is in obuf
         }
         if (seg == 1) {
 #pragma unroll
@@ -1433,59 +1521,21 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         } else if (slot > 0) {
             store_S(slot, S);
         }
-    } else {
+    } else if (w < 8) {
         // ------------------------------- output waves ------------------------------
-        struct OpsO {
-            f16x8 Qg[4];
-            bf16x8 Ah[2], Al[2];
-            float4 qsc;
-        };
-        auto load_out = [&](OpsO &op, int j) {
-            const char *rec = rec_of(j);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                op.Qg[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffQg)[(wr * 4 + s) * 64 + lane]);
-            }
-            op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 64 + 16 * wr);
-            if constexpr (!kAqChain) {
-                // rows [16wr, 16wr+16) meet columns >= 32 only for wr >= 2
-                op.Ah[0] = load_frag(rec, kOffAqH, aq_frag(wr, 0), lane);
-                op.Al[0] = load_frag(rec, kOffAqL, aq_frag(wr, 0), lane);
-                if (wr >= 2) {
-                    op.Ah[1] = load_frag(rec, kOffAqH, aq_frag(wr, 1), lane);
-                    op.Al[1] = load_frag(rec, kOffAqL, aq_frag(wr, 1), lane);
-                }
-            }
-        };
         f32x4 P[NT];  // (q e^G) S of the chunk whose output is pending
 #pragma unroll
         for (int ct = 0; ct < NT; ++ct) {
             P[ct] = z4;
         }
-        // o_j = P + Aqk vnew_j (3-pass); rows t < len of chunk j are stored,
-        // transposed through this wave's LDS tile so each lane writes CW/4
-        // consecutive columns of one row (nontemporal stores).
-        auto finish = [&](const OpsO &op, int j) {
-            const int p = j & 1;
-            uint16_t *ot = reinterpret_cast<uint16_t *>(&otile[wr][0][0]);
+        // o_j = P + Aqk vnew_j; rows t < len of chunk j are stored, transposed
+        // through this wave's LDS tile so each lane writes CW/4 consecutive
+        // columns of one row (nontemporal stores).
+        auto finish = [&](int j) {
+            uint16_t *ot = reinterpret_cast<uint16_t *>(&sm.otile[wr][0][0]);
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                f32x4 acc = P[ct];
-                if constexpr (kAqChain) {
-                    acc += obuf[p][wr][ct][lane];
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 2; ++s) {
-                        if (s == 1 && wr < 2) {
-                            break;  // Aqk is zero there (uniform per wave)
-                        }
-                        const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][0][ct][lane][0]));
-                        const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4 *>(&vbuf[p][s][1][ct][lane][0]));
-                        acc = mfma(op.Ah[s], vh, acc);
-                        acc = mfma(op.Ah[s], vl, acc);
-                        acc = mfma(op.Al[s], vh, acc);
-                    }
-                }
+                const f32x4 acc = P[ct] + sm.obuf[j & 1][wr][ct][lane];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     ot[(4 * gq + i) * CW + 16 * ct + r] = f32_to_bf16(acc[i]);
@@ -1500,7 +1550,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             uint16_t *dst = out + (static_cast<int64_t>(t0 + t) * H + h) * DK + col0 + cq * (CW / 4);
             if constexpr (NT == 1) {
                 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-                const u32x2 val = *reinterpret_cast<const u32x2 *>(&otile[wr][row][2 * cq]);
+                const u32x2 val = *reinterpret_cast<const u32x2 *>(&sm.otile[wr][row][2 * cq]);
                 if (t < len) {
                     __builtin_nontemporal_store(val, reinterpret_cast<u32x2 *>(dst));
                 }
@@ -1508,7 +1558,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 u32x4 val[NT / 2];
 #pragma unroll
                 for (int k = 0; k < NT / 2; ++k) {
-                    val[k] = *reinterpret_cast<const u32x4 *>(&otile[wr][row][(CW / 8) * cq + 4 * k]);
+                    val[k] = *reinterpret_cast<const u32x4 *>(&sm.otile[wr][row][(CW / 8) * cq + 4 * k]);
                 }
                 if (t < len) {
 #pragma unroll
@@ -1518,22 +1568,39 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         };
-        // P = (q e^G) S_j (fp16 q e^G against S_j hi + lo, one product per
-        // slice, then scaled), rows [16wr, 16wr+16)
-        auto start = [&](const OpsO &op, int j) {
-            const int p = j & 1;
-            float fq[4];
+        // q e^G rows [16wr, 16wr+16) and their scales, loaded by this wave
+        // one chunk ahead (two sets; indices past the end clamped)
+        struct OpsO {
+            f16x8 Qg[4];
+            float4 qsc;
+        };
+        auto load_out = [&](OpsO &op, int j) {
+            const char *rec = rec_of(j < j1 ? j : j1 - 1);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                fq[s] = op.qsc[s] * sscale[p][s];
+                op.Qg[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffQg)[(wr * 4 + s) * 64 + lane]);
             }
+            op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 4 * (kScQg + 4 * wr));
+        };
+        // Iteration j: [B1(j)] finish chunk j-1, load chunk j+1 into `other`,
+        // [B2(j)] P = (q e^G) S_j from `cur`: fp16 q e^G against fp16 S_j,
+        // one product per slice, then scaled.
+        auto iter = [&](const OpsO &cur, OpsO &other, int j) {
+            const int p = j & 1;
+            lds_barrier();  // B1(j)
+            if (j > j0) {
+                finish(j - 1);
+            }
+            load_out(other, j + 1);
+            lds_barrier();  // B2(j)
+            const float4 ss = *reinterpret_cast<const float4 *>(&sm.sscale[p][0]);
+            const float fq[4] = {cur.qsc.x * ss.x, cur.qsc.y * ss.y, cur.qsc.z * ss.z, cur.qsc.w * ss.w};
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
                 f32x4 acc[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    acc[s] = mfma(op.Qg[s], as_f16x8(sbuf[p][s][0][ct][lane]), z4);
-                    acc[s] = mfma(op.Qg[s], as_f16x8(sbuf[p][s][1][ct][lane]), acc[s]);
+                    acc[s] = mfma(cur.Qg[s], as_f16x8(sm.sbuf[p][s][ct][lane]), z4);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -1546,36 +1613,62 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         };
-        // Iteration j: [B1(j)] finish chunk j-1 (operands in `other`), load
-        // chunk j+1 into `other`, [B2(j)] start chunk j (operands in `cur`).
-        auto iter = [&](const OpsO &cur, OpsO &other, int j) {
-            lds_barrier();  // B1(j)
-            if (j > j0) {
-                finish(other, j - 1);
-            }
-            load_out(other, j + 1 < j1 ? j + 1 : j1 - 1);
-            lds_barrier();  // B2(j)
-            start(cur, j);
-            if (j == j1 - 1) {
-                if constexpr (kAqChain) {
-                    lds_barrier();  // B1(nch): the chain's last Aqk vnew is in obuf
-                }
-                finish(cur, j);
-            }
-        };
         OpsO opA, opB;
         if (j1 > j0) {
             load_out(opA, j0);
         }
+        lds_barrier();  // B0
+        for (int j = j0; j < j1; j += 2) {
+            iter(opA, opB, j);
+            if (j + 1 >= j1) {
+                break;
+            }
+            iter(opB, opA, j + 1);
+        }
+        if (j1 > j0) {
+            lds_barrier();  // B1(j1): the chain's last Aqk vnew is in obuf
+            finish(j1 - 1);
+        }
+    } else {
+        // ------------------------------- loader waves ------------------------------
+        // Loader wave wl carries stage fragments wl, wl + 4, ... of a chunk in
+        // registers from their load to their LDS write. Two register sets
+        // (chunks at even / odd distance from j0) keep each chunk's loads in
+        // flight for a chunk and a half: chunk c is loaded after B2(c-3) and
+        // written to the stage of its parity after B1(c-1) (every reader of
+        // that stage's previous chunk c-2 finished before B1(c-1)).
+        constexpr int kPer = St::kLoadPer;
+        const int wl = w - 8;
+        u32x4 RA[kPer], RB[kPer];
+        // Every loader wave issues the same number of loads (a surplus one
+        // repeats the last fragment, which another wave also writes with the
+        // same bytes), so the compiler's load counters stay exact and a write
+        // waits only for its own set's loads.
+        auto frag_of = [&](int k) {
+            const int f = wl + 4 * k;
+            return f < St::kFrags ? f : St::kFrags - 1;
+        };
+        auto fetch = [&](u32x4 (&R)[kPer], int j) {
+            const char *rec = rec_of(j < j1 ? j : j1 - 1);
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                R[k] = reinterpret_cast<const u32x4 *>(rec + St::src(frag_of(k), vt))[lane];
+            }
+        };
+        auto put = [&](const u32x4 (&R)[kPer], int par) {
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                reinterpret_cast<u32x4 *>(sm.stg[par] + frag_of(k) * kFrag)[lane] = R[k];
+            }
+        };
         // L2 warm-up: at chunk j each workgroup reads one dword of each line of
-        // its 1/NV share of chunk j + kWarmAhead's record (996 cache lines), so
-        // the record is in L2 before the column groups load it. Each value is
-        // folded in two chunks later, when the loads issued after it have been
-        // waited for anyway.
-        constexpr int kWarmAhead = 3;
+        // its 1/NV share of chunk j + kWarmAhead's record, so the record is in
+        // L2 before the column groups load it. Each value is folded in two
+        // chunks later, when the loads issued after it have been waited for.
+        constexpr int kWarmAhead = 4;
         constexpr int kLines = kRecBytes / 128;
         constexpr int kShare = (kLines + NV - 1) / NV;
-        constexpr int kTouch = (kShare + 255) / 256;  // lines per output lane
+        constexpr int kTouch = (kShare + 255) / 256;  // lines per loader lane
         uint32_t warm = 0, wa[kTouch], wb[kTouch];
 #pragma unroll
         for (int k = 0; k < kTouch; ++k) {
@@ -1587,21 +1680,40 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 #pragma unroll
             for (int k = 0; k < kTouch; ++k) {
                 warm ^= dst[k];
-                int i = k * 256 + wr * 64 + lane;
+                int i = k * 256 + wl * 64 + lane;
                 i = i < kShare ? i : kShare - 1;
                 int l = vt * kShare + i;
                 l = l < kLines - 1 ? l : kLines - 1;
                 dst[k] = *reinterpret_cast<const uint32_t *>(rec + l * 128);
             }
         };
+        // Chunk j+1 goes into the stage of its parity after B1(j), chunk j+3
+        // is loaded after B2(j). Indices past the end are clamped to the last
+        // chunk: the extra copies land in a stage no one reads again, and
+        // every wait count on the loop's path stays exact.
+        auto iter = [&](u32x4 (&R)[kPer], uint32_t (&dst)[kTouch], int j) {
+            lds_barrier();  // B1(j)
+            put(R, (j + 1) & 1);
+            lds_barrier();  // B2(j)
+            fetch(R, j + 3);
+            touch(dst, j + kWarmAhead);
+        };
+        if (j1 > j0) {
+            fetch(RA, j0);
+            put(RA, j0 & 1);
+            fetch(RB, j0 + 1);
+            fetch(RA, j0 + 2);
+        }
+        lds_barrier();  // B0
         for (int j = j0; j < j1; j += 2) {
-            touch(wa, j + kWarmAhead);
-            iter(opA, opB, j);
+            iter(RB, wa, j);  // writes chunk j+1 (odd distance), loads j+3
             if (j + 1 >= j1) {
                 break;
             }
-            touch(wb, j + 1 + kWarmAhead);
-            iter(opB, opA, j + 1);
+            iter(RA, wb, j + 1);  // writes chunk j+2, loads j+4
+        }
+        if (j1 > j0) {
+            lds_barrier();  // B1(j1)
         }
 #pragma unroll
         for (int k = 0; k < kTouch; ++k) {
@@ -1657,13 +1769,11 @@ int device_cus(hipStream_t stream) {
     return n;
 }
 
-// Value tiles per scan workgroup for `pairs` (sequence, head) chains. A
-// 16-column group has the shortest chunk step (≈1.5 µs on config 3 and 5) but
-// each of its workgroups reads the whole chunk record for 16 columns; a
-// 32-column group takes ≈2.1 µs per step for twice the columns. So the narrow
-// groups win while all of them run at once (pairs x 8 <= CUs), the wide ones
-// as soon as the narrow ones would need a second round (config 4: 847 -> 652
-// µs for the scan).
+// Value tiles per scan workgroup for `pairs` (sequence, head) chains: the
+// narrow groups have the shorter chunk step, the wide ones read half the
+// operand bytes per column, so the narrow ones win while all of them run at
+// once (pairs x 8 <= CUs), the wide ones as soon as the narrow ones would need
+// a second round.
 int scan_tiles(int64_t pairs, hipStream_t stream) { return pairs * 8 <= device_cus(stream) ? 1 : 2; }
 
 const void *scan_kernel(int nt, bool seg) {
@@ -1672,6 +1782,8 @@ const void *scan_kernel(int nt, bool seg) {
                    : reinterpret_cast<const void *>(chunk_scan_kernel<1, false>);
 }
 
+// 8 / nt workgroups per (sequence, head), pairs padded to a multiple of eight
+// for the XCD-aware numbering.
 int64_t scan_blocks(int64_t pairs, int nt) { return (pairs + 7) / 8 * 8 * (8 / nt); }
 
 // A second stream (default priority) and two events per device, created on

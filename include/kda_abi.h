@@ -212,8 +212,8 @@ int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,
  * KDA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; its address
  * on a device is resolved on the first call on that device. Arguments whose
  * kda_chunk_workspace_bytes exceed it return KDA_ERR_TOO_LARGE (at K = V =
- * 128 roughly 600 (chunk, head) pairs, e.g. T = 1024 tokens on 32 heads, or
- * T = 8192 on 4). Results are those of kda_chunk_launch on the same
+ * 128 roughly 750 (chunk, head) pairs, e.g. T = 1024 tokens on 32 heads, or
+ * T = 8192 on 5). Results are those of kda_chunk_launch on the same
  * arguments, always in the single-pass form (no second stream). Every call on
  * one GPU shares that GPU's array (its contents need no initialization, the
  * last call's are left behind): calls that overlap on one GPU -- concurrent

@@ -107,15 +107,15 @@ def test_chunk_launch_alignment_checks_need_no_device(lib):
 
 def test_chunk_workspace_size_formula(lib):
     """kda_chunk_workspace_bytes is a host-only function of (T, N, H, D): the
-    chunk-start table, one 108.75 KiB record per possible (chunk, head), one
-    32.5 KiB tracking record per (sequence, head) and, for a single sequence,
+    chunk-start table, one 87 KiB record per possible (chunk, head), one
+    16.75 KiB tracking record per (sequence, head) and, for a single sequence,
     one 64 KiB state per head carried between scan segments, each 256-byte
     aligned (the sizes the integration notes quote for sizing a reusable
     workspace)."""
     lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
     lib.kda_chunk_workspace_bytes.argtypes = [ctypes.c_int32] * 4
-    rec, track = 111360, 33280
-    assert rec == 108.75 * 1024 and track == 32.5 * 1024
+    rec, track = 89088, 17152
+    assert rec == 87 * 1024 and track == 16.75 * 1024
     for T, N, H in [(8192, 1, 32), (33814, 16, 32), (65536, 1, 16), (1, 1, 1), (0, 3, 2)]:
         header = ((N + 1) * 4 + 255) // 256 * 256
         max_chunks = (T + 63) // 64 + N
