@@ -1294,10 +1294,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         }
         const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
 
-        // Operands of phase B (w, u and the scalars of vnew's scale) are read
-        // from the stage a chunk ahead, during the previous chunk's phase C
-        // (the stage of chunk j+1 is complete from B2(j)); those of phase C
-        // (kd^T, Aqk, e^(G_last)) during phase B.
+        // Chunk j's operands are read from the stage after B1(j) (the loaders
+        // write it between B2(j-1) and B1(j)): those of phase B first, then
+        // those of phase C behind the first tile's S fragments.
         struct OpsB {
             f16x8 Wf[4];
             f32x4 uu[NT];
@@ -1325,7 +1324,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             const float4 wl = *reinterpret_cast<const float4 *>(sc + kScWl1);
             op.wl1 = fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w));
         };
-        auto step = [&](const OpsB &ob, OpsB &next, int j) {
+        auto step = [&](int j) {
             const int p = j & 1;
             const int len = eos - (bos + BT * j) < BT ? eos - (bos + BT * j) : BT;
             const char *st = sm.stg[p];
@@ -1365,6 +1364,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
             lds_barrier();  // B1(j)
+            OpsB ob;
+            read_b(ob, j);
             // B. vnew rows [16wr, 16wr+16) = u - w S_j (one product per slice,
             // then scaled), published as fp16 hi/lo scaled by 2^sv; tile wr is
             // half wr%2 of slice wr/2. Phase C's operands of chunk j are read
@@ -1430,9 +1431,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             // C. S_{j+1} = e^(G_last) S_j + kd^T vnew_j (fp16 kd against vnew
             // hi + lo, then both scales), one column tile at a time; the
             // tracked prefix strictly inside this chunk is taken from S_j
-            // first. The next chunk's phase-B operands are read behind the
-            // first tile's vnew (clamped: at the last chunk this rereads the
-            // current stage, which no one rewrites before B1(j+2)).
+            // first.
             const int rr = track_len - BT * j;
             const bool track_in = track_slot > 0 && rr > 0 && rr < len;
 #pragma unroll
@@ -1442,9 +1441,6 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 for (int s = 0; s < 2; ++s) {
                     vh[s] = as_f16x8(sm.vbuf[p][s][0][ct][lane]);
                     vl[s] = as_f16x8(sm.vbuf[p][s][1][ct][lane]);
-                }
-                if (ct == 0) {
-                    read_b(next, j + 1 < j1 ? j + 1 : j);
                 }
                 if (track_in) {
                     const float *tsc = reinterpret_cast<const float *>(tr + kTrOffSc);
@@ -1495,16 +1491,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         };
 
         lds_barrier();  // B0: the first chunk's stage is written
-        OpsB obA, obB;
-        if (j1 > j0) {
-            read_b(obA, j0);
-        }
-        for (int j = j0; j < j1; j += 2) {
-            step(obA, obB, j);
-            if (j + 1 >= j1) {
-                break;
-            }
-            step(obB, obA, j + 1);
+        for (int j = j0; j < j1; ++j) {
+            step(j);
         }
         if (j1 > j0) {
             lds_barrier();  // B1(j1): the last Aqk vnew is in obuf
@@ -1582,17 +1570,18 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
             op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 4 * (kScQg + 4 * wr));
         };
-        // Iteration j: [B1(j)] finish chunk j-1, load chunk j+1 into `other`,
-        // [B2(j)] P = (q e^G) S_j from `cur`: fp16 q e^G against fp16 S_j,
-        // one product per slice, then scaled.
+        // Iteration j: [B1(j)] load chunk j+1 into `other`, [B2(j)] finish
+        // chunk j-1 (its Aqk vnew is in obuf since B2(j-1) and is rewritten
+        // only after B2(j+1)), then P = (q e^G) S_j from `cur`: fp16 q e^G
+        // against fp16 S_j, one product per slice, then scaled.
         auto iter = [&](const OpsO &cur, OpsO &other, int j) {
             const int p = j & 1;
             lds_barrier();  // B1(j)
+            load_out(other, j + 1);
+            lds_barrier();  // B2(j)
             if (j > j0) {
                 finish(j - 1);
             }
-            load_out(other, j + 1);
-            lds_barrier();  // B2(j)
             const float4 ss = *reinterpret_cast<const float4 *>(&sm.sscale[p][0]);
             const float fq[4] = {cur.qsc.x * ss.x, cur.qsc.y * ss.y, cur.qsc.z * ss.z, cur.qsc.w * ss.w};
 #pragma unroll
@@ -1634,9 +1623,10 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // Loader wave wl carries stage fragments wl, wl + 4, ... of a chunk in
         // registers from their load to their LDS write. Two register sets
         // (chunks at even / odd distance from j0) keep each chunk's loads in
-        // flight for a chunk and a half: chunk c is loaded after B2(c-3) and
-        // written to the stage of its parity after B1(c-1) (every reader of
-        // that stage's previous chunk c-2 finished before B1(c-1)).
+        // flight for a chunk and a half: chunk c is loaded after B1(c-2) and
+        // written to the stage of its parity after B2(c-1) (every reader of
+        // that stage's previous chunk c-2 finished before B2(c-1): the chain
+        // reads a stage between B1 and B2 of its chunk).
         constexpr int kPer = St::kLoadPer;
         const int wl = w - 8;
         u32x4 RA[kPer], RB[kPer];
@@ -1687,30 +1677,30 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 dst[k] = *reinterpret_cast<const uint32_t *>(rec + l * 128);
             }
         };
-        // Chunk j+1 goes into the stage of its parity after B1(j), chunk j+3
-        // is loaded after B2(j). Indices past the end are clamped to the last
-        // chunk: the extra copies land in a stage no one reads again, and
-        // every wait count on the loop's path stays exact.
-        auto iter = [&](u32x4 (&R)[kPer], uint32_t (&dst)[kTouch], int j) {
+        // Chunk j+2 is loaded after B1(j) into the set chunk j left (written
+        // after B2(j-1)), chunk j+1 goes into the stage of its parity after
+        // B2(j). Indices past the end are clamped to the last chunk: the extra
+        // copies land in a stage no one reads again, and every wait count on
+        // the loop's path stays exact.
+        auto iter = [&](u32x4 (&Rload)[kPer], const u32x4 (&Rput)[kPer], uint32_t (&dst)[kTouch], int j) {
             lds_barrier();  // B1(j)
-            put(R, (j + 1) & 1);
-            lds_barrier();  // B2(j)
-            fetch(R, j + 3);
+            fetch(Rload, j + 2);
             touch(dst, j + kWarmAhead);
+            lds_barrier();  // B2(j)
+            put(Rput, (j + 1) & 1);
         };
         if (j1 > j0) {
             fetch(RA, j0);
             put(RA, j0 & 1);
             fetch(RB, j0 + 1);
-            fetch(RA, j0 + 2);
         }
         lds_barrier();  // B0
         for (int j = j0; j < j1; j += 2) {
-            iter(RB, wa, j);  // writes chunk j+1 (odd distance), loads j+3
+            iter(RA, RB, wa, j);  // loads chunk j+2 (even distance), writes j+1
             if (j + 1 >= j1) {
                 break;
             }
-            iter(RA, wb, j + 1);  // writes chunk j+2, loads j+4
+            iter(RB, RA, wb, j + 1);  // loads j+3, writes j+2
         }
         if (j1 > j0) {
             lds_barrier();  // B1(j1)
