@@ -233,9 +233,11 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
     auto koff = [&](int j) { return 4 * kc + 4 * L * j; };
     const int64_t head_off = static_cast<int64_t>(head) * a.state_stride_head;
     // A [K,V]-contiguous pool (state_v_contiguous, the prepared_recurrent
-    // layout of the reference) is read and written in place element by
-    // element: element (k, v) of a slot and head sits at k*D + v.
-    const bool vpool = a.state_v_contiguous != 0;
+    // layout of the reference; DECAY mode only, the launcher rejects it
+    // otherwise, so the other modes compile without it) is read and written
+    // in place element by element: element (k, v) of a slot and head sits at
+    // k*D + v.
+    const bool vpool = GATE == KDA_GATE_DECAY && a.state_v_contiguous != 0;
     float4 S[NP][EV];
     if (slot > 0) {
         const float *src = a.state + slot * a.state_stride_slot + head_off;
@@ -597,6 +599,9 @@ extern "C" int kda_recurrent_launch(const KdaRecurrentArgs *args, void *stream) 
     const int D = a.head_dim;
     if (D != 64 && D != 128) {
         return KDA_ERR_UNSUPPORTED;
+    }
+    if (a.state_v_contiguous != 0 && a.gate_mode != KDA_GATE_DECAY) {
+        return KDA_ERR_UNSUPPORTED;  // the [K,V] pool is the prepared (DECAY) layout
     }
     if (a.num_seqs < 0 || a.num_tokens < 0 || a.num_heads <= 0 || a.num_slots < 0) {
         return KDA_ERR_INVALID_ARGUMENT;

@@ -157,9 +157,14 @@ def timed(step, steps, warmup, min_settle):
 # ---------------------------------------------------------------------------
 
 
-def source_sha256(names=("kda_recurrent.hip", "kda_chunk.hip", "kda_device.h")):
-    """sha256 over the kernel sources, in order (the key the profile summaries
-    record, so a figure measured on other kernels is never reported)."""
+DECODE_SOURCES = ("kda_recurrent.hip", "kda_device.h")
+PREFILL_SOURCES = ("kda_chunk.hip", "kda_device.h")
+
+
+def source_sha256(names):
+    """sha256 over the given kernel sources, in order (the key the profile
+    summaries record, so a figure measured on other kernels is never
+    reported)."""
     h = hashlib.sha256()
     for n in names:
         with open(os.path.join(CSRC, n), "rb") as f:
@@ -492,19 +497,21 @@ def run_latency_rows(steps, check):
 
 
 def summarize_trace(path, last):
-    """Per-kernel duration statistics from a rocprofv3 kernel-trace CSV over
-    each kernel's last ``last`` dispatches (0 = all)."""
+    """Per-kernel duration statistics from a rocprofv3 kernel-trace CSV, one
+    row per (kernel, grid size) -- the grid tells the workloads of one kernel
+    apart -- over each row's last ``last`` dispatches (0 = all)."""
     by = {}
     with open(path) as f:
         for row in csv.DictReader(f):
             us = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
-            by.setdefault(row["Kernel_Name"], []).append((int(row["Dispatch_Id"]), us))
-    print(f"| kernel | dispatches | used | mean µs | median µs | min µs | max µs |")
-    print("|---|---|---|---|---|---|---|")
-    for name, xs in sorted(by.items(), key=lambda kv: -sum(u for _, u in kv[1])):
+            key = (row["Kernel_Name"], int(row["Grid_Size_X"]))
+            by.setdefault(key, []).append((int(row["Dispatch_Id"]), us))
+    print("| kernel | grid | dispatches | used | mean µs | median µs | min µs | max µs |")
+    print("|---|---|---|---|---|---|---|---|")
+    for (name, grid), xs in sorted(by.items(), key=lambda kv: -sum(u for _, u in kv[1])):
         xs.sort()
         sel = [u for _, u in (xs[-last:] if last > 0 else xs)]
-        print(f"| `{name[:110]}` | {len(xs)} | {len(sel)} | {statistics.mean(sel):.2f} | "
+        print(f"| `{name[:100]}` | {grid} | {len(xs)} | {len(sel)} | {statistics.mean(sel):.2f} | "
               f"{statistics.median(sel):.2f} | {min(sel):.2f} | {max(sel):.2f} |")
 
 
@@ -576,7 +583,8 @@ def main():
 
     ops = torch.ops.sgl_glm53_ascend
     check = not args.no_cpu
-    sha = source_sha256()
+    dec_sha = source_sha256(DECODE_SOURCES)
+    pf_sha = source_sha256(PREFILL_SOURCES)
     validated = {}
     failed = False
 
@@ -656,7 +664,7 @@ def main():
         pf = timed(pstep, max(5, args.steps // 2), args.warmup, (2 * args.settle) // 3)
         us = pf["event_us_per_call"]
         tf = PF_FLOP / (us * 1e-6) / 1e12
-        traffic, traffic_src = traffic_from_profile("prefill_chunk_t8192_h32_hbm_traffic.md", sha)
+        traffic, traffic_src = traffic_from_profile("prefill_chunk_t8192_h32_hbm_traffic.md", pf_sha)
         prefill = dict(
             workload="chunk prefill T=8192 H=32 K=V=128 BT=64 bf16 qkv, fp32 g/beta/state",
             tok_per_s=PF_T / (pf["ms_per_step"] / 1e3),
@@ -672,6 +680,7 @@ def main():
             algorithmic_bytes=PF_BYTES,
             traffic=traffic,
             traffic_source=traffic_src,
+            source_sha256=pf_sha,
             workspace_bytes=int(sgl_glm53_ascend_ops.chunk_workspace_bytes(PF_T, 1, PF_H)),
             cpu_baseline=pf_cpu,
         )
@@ -693,7 +702,7 @@ def main():
         return
     tok_s = DEC_N / (dec["ms_per_step"] / 1e3)
     achieved = DEC_BYTES / (dec["event_us_per_call"] * 1e-6) / 1e9
-    traffic, traffic_src = traffic_from_profile("decode_recurrent_b256_h32_hbm_traffic.md", sha)
+    traffic, traffic_src = traffic_from_profile("decode_recurrent_b256_h32_hbm_traffic.md", dec_sha)
     line = dict(
         metric="KDA decode tok/s + state HBM GB/s (B=256); chunk prefill tok/s (T=8k)",
         value=tok_s,
@@ -722,7 +731,7 @@ def main():
             kernel="recurrent_kernel<128,32,2,strided rows,decode,bf16,bf16,LOG>",
             algorithmic_bytes_per_launch=DEC_BYTES,
             event_us_per_call=dec["event_us_per_call"],
-            source_sha256=sha,
+            source_sha256=dec_sha,
         ),
         prefill=prefill,
         more_configs=more,

@@ -131,7 +131,8 @@ typedef struct KdaRecurrentArgs {
     /* State pool layout: 0 = K contiguous (the layout contract above); 1 =
      * [K,V] contiguous, element (s, h, k, v) at
      * state[s*state_stride_slot + h*state_stride_head + k*D + v] (the
-     * prepared_recurrent pool of the reference), read and written in place.
+     * prepared_recurrent pool of the reference), read and written in place;
+     * KDA_GATE_DECAY only (KDA_ERR_UNSUPPORTED with the other gate modes).
      * Checkpoints (`intermediate`) are K contiguous either way. */
     int32_t state_v_contiguous;
 } KdaRecurrentArgs;

@@ -59,6 +59,45 @@ def test_argument_checks_return_before_any_device_call(lib):
     assert lib.kda_chunk_launch(None, None, 0, None) != 0
 
 
+class _RecArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p), ("beta", ctypes.c_void_p),
+        ("A_log", ctypes.c_void_p), ("dt_bias", ctypes.c_void_p),
+        ("state", ctypes.c_void_p), ("state_stride_slot", ctypes.c_int64),
+        ("state_stride_head", ctypes.c_int64), ("num_slots", ctypes.c_int64),
+        ("state_indices", ctypes.c_void_p), ("cu_seqlens", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("intermediate", ctypes.c_void_p), ("mid_stride_req", ctypes.c_int64),
+        ("mid_stride_step", ctypes.c_int64), ("mid_stride_head", ctypes.c_int64),
+        ("mid_rows", ctypes.c_int64), ("mid_steps", ctypes.c_int64),
+        ("track_indices", ctypes.c_void_p), ("track_lens", ctypes.c_void_p),
+        ("scale", ctypes.c_float), ("lower_bound", ctypes.c_float),
+        ("num_seqs", ctypes.c_int32), ("num_tokens", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32), ("head_begin", ctypes.c_int32),
+        ("head_count", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("qk_dtype", ctypes.c_int32), ("v_dtype", ctypes.c_int32),
+        ("gate_mode", ctypes.c_int32), ("qk_l2norm", ctypes.c_int32),
+        ("state_v_contiguous", ctypes.c_int32),
+    ]
+
+
+def test_v_contiguous_pool_only_in_decay_mode(lib):
+    """A [K,V]-contiguous pool is the prepared (DECAY) layout: with the RAW or
+    LOG gate the launcher returns KDA_ERR_UNSUPPORTED before touching the
+    device (the addresses are never dereferenced)."""
+    lib.kda_recurrent_launch.restype = ctypes.c_int
+    lib.kda_recurrent_launch.argtypes = [ctypes.POINTER(_RecArgs), ctypes.c_void_p]
+    base = 1 << 20
+    for gate in (0, 1):  # KDA_GATE_RAW, KDA_GATE_LOG
+        a = _RecArgs(q=base, k=base, v=base, gate=base, beta=base, A_log=base, dt_bias=base,
+                     state=base, state_stride_slot=32 * 128 * 128, state_stride_head=128 * 128,
+                     num_slots=4, state_indices=base, cu_seqlens=base, out=base, scale=1.0,
+                     num_seqs=1, num_tokens=1, num_heads=32, head_dim=128, gate_mode=gate,
+                     state_v_contiguous=1)
+        assert lib.kda_recurrent_launch(ctypes.byref(a), None) == 2, gate  # KDA_ERR_UNSUPPORTED
+
+
 class _ChunkArgs(ctypes.Structure):
     _fields_ = [
         ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
