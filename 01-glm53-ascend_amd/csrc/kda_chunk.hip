@@ -94,8 +94,8 @@ constexpr int kScW = 0;      // [16] w fragment (mt, s): mt * 4 + s
 constexpr int kScQg = 16;    // [16] q e^G fragment (mt, s)
 constexpr int kScKd = 32;    // [8]  kd^T row tile mk (both token slices)
 constexpr int kScAq = 40;    // [4]  Aqk row tile mt (both token slices)
-constexpr int kScUmax = 44;  // [32] max |u| over row tile mt, column tile vt: mt * 8 + vt
-constexpr int kScWl1 = 76;   // [4]  max over the rows of tile mt of sum_k |w[t][k]|
+constexpr int kScUmax = 44;  // [4]  max |u| over row tile mt (all 128 columns)
+constexpr int kScWl1 = 48;   // [4]  max over the rows of tile mt of sum_k |w[t][k]|
 // Track record of one (sequence, head): operands of the state after r < len
 // tokens of the chunk holding the tracked position.
 constexpr int kTrOffKd = 0;                       // fp16, scaled per row tile mk
@@ -355,16 +355,19 @@ __device__ __forceinline__ uint32_t keep_mask(bool keep) {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-// MFMA operand from a row-major bf16 LDS tile whose rows are the K index:
-// lane (r, g) receives tile[row0 + kperm(g, e)][col0 + r], e = 0..7 (two
-// transposing reads, rows row0 + 4g + m and row0 + 16 + 4g + m).
+// MFMA operand from a row-major bf16 LDS tile (row stride PAD elements, a
+// multiple of 4) whose rows are the K index: lane (r, g) receives
+// tile[row0 + kperm(g, e)][col0 + r], e = 0..7 (two transposing reads, rows
+// row0 + 4g + m and row0 + 16 + 4g + m).
+template <int PAD = kPadT>
 __device__ __forceinline__ bf16x8 lds_tr_frag(const uint16_t *tile, int row0, int col0, int lane) {
+    static_assert(PAD % 4 == 0, "8-byte aligned rows");
     const int g = lane >> 4;
     const int m = (lane >> 2) & 3;
     const int c4 = lane & 3;
-    const uint16_t *p0 = tile + (row0 + 4 * g + m) * kPadT + col0 + 4 * c4;
+    const uint16_t *p0 = tile + (row0 + 4 * g + m) * PAD + col0 + 4 * c4;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0 + 16 * kPadT));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0 + 16 * PAD));
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
@@ -624,9 +627,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     }
     lds_barrier();
 
-    auto kval = [&](int t, int k) {
-        return bf16_to_f32(sm.u.early.K[t][k]) * sm.rnk[t];
-    };
     // 8 channels {32s + kperm(gq, e)} of one row: two 8-byte k reads, two
     // 16-byte G reads.
     auto load_k8 = [&](int row, int s, float x[8]) {
@@ -738,6 +738,18 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     }
 
     // ---- S4: kd^T fragments, e^(G_last), tracking operands, e^G k ----------
+    // k[t][16mk + r] rnk[t] for the rows t = 32s + kperm(gq, e) of a kd^T
+    // fragment: k by transposing reads, the row scales as two float4 reads.
+    auto kd_rows = [&](int s, int mk, float (&kr)[8]) {
+        const bf16x8 kb = lds_tr_frag<kPadK>(&sm.u.early.K[0][0], 32 * s, 16 * mk, lane);
+        const float4 rn0 = *reinterpret_cast<const float4 *>(&sm.rnk[32 * s + 4 * gq]);
+        const float4 rn1 = *reinterpret_cast<const float4 *>(&sm.rnk[32 * s + 16 + 4 * gq]);
+        const float rn[8] = {rn0.x, rn0.y, rn0.z, rn0.w, rn1.x, rn1.y, rn1.z, rn1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            kr[e] = static_cast<float>(kb[e]) * rn[e];
+        }
+    };
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         const int mk = 2 * wave + tt;
@@ -746,10 +758,12 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         float x[2][8];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
+            float kr[8];
+            kd_rows(s, mk, kr);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int t = 32 * s + kperm(gq, e);
-                x[s][e] = kval(t, k) * ex2(gl - sm.u.early.G[t][k]);
+                x[s][e] = kr[e] * ex2(gl - sm.u.early.G[t][k]);
             }
         }
         store_frags_f16<2>(rec, kOffKd, mk * 2, reinterpret_cast<float *>(rec + kOffSc) + kScKd + mk, lane, x);
@@ -773,10 +787,12 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 float x[2][8];
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
+                    float kr[8];
+                    kd_rows(s, mk, kr);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int t = 32 * s + kperm(gq, e);
-                        x[s][e] = t < rr ? kval(t, k) * ex2(gr - sm.u.early.G[t][k]) : 0.f;
+                        x[s][e] = t < rr ? kr[e] * ex2(gr - sm.u.early.G[t][k]) : 0.f;
                     }
                 }
                 store_frags_f16<2>(tr, kTrOffKd, mk * 2, reinterpret_cast<float *>(tr + kTrOffSc) + mk, lane, x);
@@ -852,13 +868,14 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         const int t = rg + 8 * i;
         *reinterpret_cast<uint2 *>(&sm.u.mid.KE[t][4 * kc]) = kep[i];
     }
-    // X: upper blocks zero
-    for (int idx = tid; idx < BT * BT; idx += kThreads) {
-        const int i = idx >> 6;
-        const int j = idx & 63;
-        if ((j >> 4) > (i >> 4)) {
-            sm.u.mid.X[i][j] = 0.f;
-        }
+    // X: the six upper 16x16 blocks (I, J > I) zero, one float4 per store
+    for (int f = tid; f < 6 * 64; f += kThreads) {
+        const int blk = f >> 6;                      // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+        const int bi = blk < 3 ? 0 : (blk < 5 ? 1 : 2);
+        const int bj = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
+        const int row = (f & 63) >> 2;
+        *reinterpret_cast<float4 *>(&sm.u.mid.X[16 * bi + row][16 * bj + 4 * (f & 3)]) =
+            make_float4(0.f, 0.f, 0.f, 0.f);
     }
     lds_barrier();
     if (sh == 0) {
@@ -922,7 +939,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
     }
 
-    // ---- S5: X = (I + L)^-1 (blocked, fp32), then T = X diag(beta) ----------
+    // ---- S5: X = (I + L)^-1 (blocked, fp32); T = X diag(beta) is formed as S6 reads X
     // Diagonal 16x16 blocks, right-looking: column c of block w per lane c.
     if (lane < 16) {
         const int b0 = 16 * wave;
@@ -1002,12 +1019,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
         lds_barrier();
     }
-    for (int idx = tid; idx < BT * BT; idx += kThreads) {
-        const int i = idx >> 6;
-        const int j = idx & 63;
-        sm.u.mid.X[i][j] *= sm.beta[j];
-    }
-    lds_barrier();
 
     // ---- S6: u = T v (T split) and w^T = (e^G k)^T T^T (single) --------------
     {
@@ -1016,9 +1027,13 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         bf16x8 Th[2], Tl[2];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
+            // T = X diag(beta), row t, columns 32s + kperm(gq, e)
             const float4 x0 = *reinterpret_cast<const float4 *>(&sm.u.mid.X[t][32 * s + 4 * gq]);
             const float4 x1 = *reinterpret_cast<const float4 *>(&sm.u.mid.X[t][32 * s + 16 + 4 * gq]);
-            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const float4 b0 = *reinterpret_cast<const float4 *>(&sm.beta[32 * s + 4 * gq]);
+            const float4 b1 = *reinterpret_cast<const float4 *>(&sm.beta[32 * s + 16 + 4 * gq]);
+            const float x[8] = {x0.x * b0.x, x0.y * b0.y, x0.z * b0.z, x0.w * b0.w,
+                                x1.x * b1.x, x1.y * b1.y, x1.z * b1.z, x1.w * b1.w};
             split_bf16x8(x, Th[s], Tl[s]);
         }
         // v goes over the dead X and LT once every wave holds its T rows
@@ -1029,6 +1044,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
         lds_barrier();
         // u tiles (mt = wave, vt): A = T rows, B = v (K = token)
+        float um = 0.f;
 #pragma unroll
         for (int vt = 0; vt < 8; ++vt) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1042,11 +1058,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 acc = mfma(Tl[s], vb, acc);
             }
             reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = acc;
-            const float um = wave_max(fmaxf(fmaxf(fabsf(acc[0]), fabsf(acc[1])),
-                                            fmaxf(fabsf(acc[2]), fabsf(acc[3]))));
-            if (lane == 0) {
-                reinterpret_cast<float *>(rec + kOffSc)[kScUmax + wave * 8 + vt] = um;
-            }
+            um = fmaxf(um, fmaxf(fmaxf(fabsf(acc[0]), fabsf(acc[1])), fmaxf(fabsf(acc[2]), fabsf(acc[3]))));
+        }
+        um = wave_max(um);
+        if (lane == 0) {
+            reinterpret_cast<float *>(rec + kOffSc)[kScUmax + wave] = um;
         }
         // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k (K = token), B = T^T;
         // wl1 sums |w| over this lane's columns of row 16 wave + r
@@ -1310,16 +1326,12 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             for (int s = 0; s < 4; ++s) {
                 op.Wf[s] = stage_frag(st, wr * 4 + s, lane);
             }
-            float um = 0.f;
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
                 op.uu[ct] = reinterpret_cast<const f32x4 *>(st + (kStU + wr * NT + ct) * kFrag)[lane];
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-                    um = fmaxf(um, sc[kScUmax + mt * 8 + NT * vt + ct]);
-                }
             }
-            op.umax = um;
+            const float4 um = *reinterpret_cast<const float4 *>(sc + kScUmax);
+            op.umax = fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w));
             op.wsc = *reinterpret_cast<const float4 *>(sc + kScW + 4 * wr);
             const float4 wl = *reinterpret_cast<const float4 *>(sc + kScWl1);
             op.wl1 = fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w));
