@@ -106,7 +106,7 @@ static_assert(kRecBytes % 256 == 0 && kTrBytes % 256 == 0, "records stay 256-B a
 
 struct Layout {
     size_t chunk_start;  // int32 [N+1]
-    size_t recs;         // kRecBytes x (max_chunks x H)
+    size_t recs;         // kRecBytes x (ring x H): chunk c's record in ring slot c % ring
     size_t tracks;       // kTrBytes x (N x H)
     size_t carry;        // one sequence: fp32 [H][V][K], the state between scan segments
     size_t total;
@@ -120,22 +120,18 @@ __host__ __device__ inline int max_chunks(int T, int N) { return (T + BT - 1) / 
 // columns >= 32) are zero and not stored, leaving six per record.
 __host__ __device__ constexpr int aq_frag(int mt, int s) { return mt < 2 ? mt : 2 * mt - 2 + s; }
 
-__host__ __device__ inline Layout layout(int T, int N, int H) {
+// ring: record slots per head; every chunk has its own slot when ring >=
+// max_chunks (the one-pass layout), a window ring of 2W slots otherwise.
+__host__ __device__ inline Layout layout(int T, int N, int H, int ring) {
     Layout L;
     L.chunk_start = 0;
     L.recs = align256(static_cast<size_t>(N + 1) * 4);
-    L.tracks = L.recs + static_cast<size_t>(kRecBytes) * max_chunks(T, N) * H;
+    L.tracks = L.recs + static_cast<size_t>(kRecBytes) * ring * H;
     L.carry = L.tracks + static_cast<size_t>(kTrBytes) * N * H;
     L.total = L.carry + (N == 1 ? static_cast<size_t>(DK) * DK * 4 * H : 0);
     return L;
 }
-
-// A long single sequence whose scan would leave half the CUs idle is run in
-// two segments: K1 of the second segment overlaps the first segment's scan
-// on a second stream (segment 0 = the whole sequence). The first segment
-// holds this many of the sequence's nch chunks (~47%: the best of 35-62%
-// measured on config 5).
-__host__ __device__ inline int split_chunk(int nch) { return (nch * 47 + 50) / 100; }
+__host__ __device__ inline Layout layout(int T, int N, int H) { return layout(T, N, H, max_chunks(T, N)); }
 
 __device__ __forceinline__ int kperm(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
 
@@ -395,35 +391,38 @@ struct PrepShared {
 };
 static_assert(sizeof(PrepShared) <= 54 * 1024, "the prepare kernel's LDS budget");
 
+// Chunks [c_lo, c_hi) of the launch (global chunk indices: one sequence's
+// own chunks, or all sequences' through the chunk index); chunk c's record
+// goes to ring slot c % ring.
 template <int GATE>
 __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkArgs a, char *ws,
-                                                                 int nrec, int seg) {
+                                                                 int ring, int c_lo, int c_hi) {
     __shared__ PrepShared sm;
     // Workgroups run chunk-descending, heads fastest: the scan starts with the
     // first chunk of every sequence and head, so those records are written
     // last and are still in the memory-side cache when it reads them (plain
     // write-back stores; with this order they beat nontemporal ones by 2%).
     const int H = a.num_heads;
-    const int c = (nrec - 1) - static_cast<int>(blockIdx.x) / H;
+    const int c = (c_hi - 1) - static_cast<int>(blockIdx.x) / H;
     const int h = static_cast<int>(blockIdx.x) % H;
     const int N = a.num_seqs;
-    const Layout LY = layout(a.num_tokens, N, H);
+    const Layout LY = layout(a.num_tokens, N, H, ring);
     int n = 0;
     int jc = c;
     int bos, eos;
+    if (c < c_lo) {
+        return;
+    }
     if (N == 1) {
         // one sequence: chunk c is its c-th (no chunk-index pass ran)
         seq_bounds(a, 0, bos, eos);
         const int nch = (eos - bos + BT - 1) / BT;
-        if (c >= nch || c >= nrec) {
+        if (c >= nch) {
             return;
-        }
-        if (seg != 0 && (c < split_chunk(nch)) != (seg == 1)) {
-            return;  // the other segment's chunk
         }
     } else {
         const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
-        if (c >= cs[N] || c >= nrec) {
+        if (c >= cs[N]) {
             return;
         }
         int lo = 0, hi = N - 1;
@@ -447,7 +446,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     const int wave = tid >> 6;
     const int r = lane & 15;
     const int gq = lane >> 4;
-    char *rec = ws + LY.recs + (static_cast<size_t>(c) * H + h) * kRecBytes;
+    char *rec = ws + LY.recs + (static_cast<size_t>(c % ring) * H + h) * kRecBytes;
     const bool norm = GATE == KDA_GATE_RAW || a.qk_l2norm != 0;
     const uint16_t *qp = static_cast<const uint16_t *>(a.q);
 
@@ -1198,13 +1197,15 @@ __device__ __forceinline__ void split_f16x2(float x0, float x1, int sh, uint32_t
                    static_cast<_Float16>(a1 - static_cast<float>(h1)));
 }
 
-// SEG: the two-segment form (seg_arg 1 or 2); without it every launch scans
-// the whole sequence and the segment logic compiles away.
+// SEG: one segment [s_lo, s_hi) of a single sequence's chunks (the state
+// comes from the pool in the first segment and from the carry area after,
+// goes to the carry area until the segment that holds the last chunk);
+// without it every launch scans whole sequences and the segment logic
+// compiles away. Chunk c's record is in ring slot c % ring.
 template <int NT, bool SEG>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws,
-                                                                  int seg_arg) {
+                                                                  int ring, int s_lo, int s_hi) {
     using St = Stage<NT>;
-    const int seg = SEG ? seg_arg : 0;
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
     __shared__ ScanShared<NT> sm;
@@ -1224,16 +1225,29 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     }
     const int n = pair / H;
     const int h = pair - n * H;
-    const Layout LY = layout(a.num_tokens, N, H);
+    const Layout LY = layout(a.num_tokens, N, H, ring);
     const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
     int bos, eos;
     seq_bounds(a, n, bos, eos);
     // one sequence: its records start at 0 (no chunk-index pass ran)
     const int c0 = N == 1 ? 0 : cs[n];
     const int nch = N == 1 ? (eos - bos + BT - 1) / BT : cs[n + 1] - c0;
-    // chunks [j0, j1) of this launch (segments 1 and 2: one sequence only)
-    const int j0 = seg == 2 ? split_chunk(nch) : 0;
-    const int j1 = seg == 1 ? split_chunk(nch) : nch;
+    // chunks [j0, j1) of this launch; `first` takes the state from the pool
+    // (and writes the rows before the sequence), `last` stores it (and the
+    // rows after); a segment past the sequence's end does nothing
+    int j0 = 0;
+    int j1 = nch;
+    bool first = true;
+    bool last = true;
+    if constexpr (SEG) {
+        if (s_lo >= nch && !(s_lo == 0 && nch == 0)) {
+            return;
+        }
+        j0 = s_lo;
+        j1 = s_hi < nch ? s_hi : nch;
+        first = s_lo == 0;
+        last = s_hi >= nch;
+    }
     float *carry = reinterpret_cast<float *>(const_cast<char *>(ws) + LY.carry) +
                    static_cast<size_t>(h) * DK * DK;
 
@@ -1248,8 +1262,13 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     const int col0 = CW * vt;  // first value column of this group
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
     uint16_t *out = static_cast<uint16_t *>(a.out);
+    // ring slot of chunk j: the launch's chunks are consecutive and at most a
+    // ring apart from its first, so one wrap suffices past (c0 + j0) % ring
+    const int slot0 = (c0 + j0) % ring;
     auto rec_of = [&](int j) {
-        return ws + LY.recs + (static_cast<size_t>(c0 + j) * H + h) * kRecBytes;
+        int sl = slot0 + (j - j0);
+        sl = sl >= ring ? sl - ring : sl;
+        return ws + LY.recs + (static_cast<size_t>(sl) * H + h) * kRecBytes;
     };
 
     if (w < 4) {
@@ -1284,7 +1303,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                if (seg == 2) {
+                if (!first) {
                     const float4 s4 = load4(carry_ptr(tt, ct));
                     S[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
                 } else if (slot > 0) {
@@ -1305,7 +1324,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         };
-        if (track_slot > 0 && track_len == 0 && seg != 2) {
+        if (track_slot > 0 && track_len == 0 && first) {
             store_S(track_slot, S);
         }
         const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
@@ -1509,7 +1528,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         if (j1 > j0) {
             lds_barrier();  // B1(j1): the last Aqk vnew is in obuf
         }
-        if (seg == 1) {
+        if (!last) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
@@ -1738,10 +1757,10 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
         }
     };
-    if (n == 0 && seg != 2) {
+    if (n == 0 && first) {
         zero_rows(0, bos);
     }
-    if (n == N - 1 && seg != 1) {
+    if (n == N - 1 && last) {
         zero_rows(eos, a.num_tokens);
     }
 }
@@ -1779,24 +1798,29 @@ int device_cus(hipStream_t stream) {
 int scan_tiles(int64_t pairs, hipStream_t stream) { return pairs * 8 <= device_cus(stream) ? 1 : 2; }
 
 const void *scan_kernel(int nt, bool seg) {
-    return nt == 2 ? reinterpret_cast<const void *>(chunk_scan_kernel<2, false>)
-           : seg   ? reinterpret_cast<const void *>(chunk_scan_kernel<1, true>)
-                   : reinterpret_cast<const void *>(chunk_scan_kernel<1, false>);
+    if (nt == 2) {
+        return seg ? reinterpret_cast<const void *>(chunk_scan_kernel<2, true>)
+                   : reinterpret_cast<const void *>(chunk_scan_kernel<2, false>);
+    }
+    return seg ? reinterpret_cast<const void *>(chunk_scan_kernel<1, true>)
+               : reinterpret_cast<const void *>(chunk_scan_kernel<1, false>);
 }
 
 // 8 / nt workgroups per (sequence, head), pairs padded to a multiple of eight
 // for the XCD-aware numbering.
 int64_t scan_blocks(int64_t pairs, int nt) { return (pairs + 7) / 8 * 8 * (8 / nt); }
 
-// A second stream (default priority) and two events per device, created on
-// first use and kept for the process: the split prefill forks K1 of its
-// second segment onto the stream and joins it back before the second scan.
-// `order` is held across one call's fork / join sequence, so calls from
-// several host threads cannot interleave their event records and waits.
+// A second stream (default priority) and four events per device, created on
+// first use and kept for the process: the segmented prefill runs K1 of
+// segment s+1 on the stream while the scan of segment s runs on the caller's
+// (`done1[s&1]` after each K1, waited for by the scan; `done2[s&1]` recorded
+// on the caller's stream just before each scan, waited for by the next K1).
+// `order` is held across one call's sequence, so calls from several host
+// threads cannot interleave their records and waits.
 struct SideStream {
     hipStream_t stream = nullptr;
-    hipEvent_t fork = nullptr;
-    hipEvent_t join = nullptr;
+    hipEvent_t done1[2] = {nullptr, nullptr};
+    hipEvent_t done2[2] = {nullptr, nullptr};
     std::mutex *order = nullptr;
 };
 
@@ -1830,10 +1854,12 @@ bool side_stream(hipStream_t main, SideStream &out) {
             return false;
         }
         SideStream fresh;
-        const bool ok = hipSetDevice(dev) == hipSuccess &&
-                        hipStreamCreateWithFlags(&fresh.stream, hipStreamNonBlocking) == hipSuccess &&
-                        hipEventCreateWithFlags(&fresh.fork, hipEventDisableTiming) == hipSuccess &&
-                        hipEventCreateWithFlags(&fresh.join, hipEventDisableTiming) == hipSuccess;
+        bool ok = hipSetDevice(dev) == hipSuccess &&
+                  hipStreamCreateWithFlags(&fresh.stream, hipStreamNonBlocking) == hipSuccess;
+        for (int i = 0; i < 2 && ok; ++i) {
+            ok = hipEventCreateWithFlags(&fresh.done1[i], hipEventDisableTiming) == hipSuccess &&
+                 hipEventCreateWithFlags(&fresh.done2[i], hipEventDisableTiming) == hipSuccess;
+        }
         (void)hipSetDevice(cur);
         if (!ok) {
             (void)hipGetLastError();
@@ -1846,11 +1872,60 @@ bool side_stream(hipStream_t main, SideStream &out) {
     return true;
 }
 
-// Single sequences at least this long whose scan fills at most half the CUs
-// take the two-segment path (measured: T = 8192 loses 8-9 µs to the extra
-// launches and the fork / join, T = 16384 on 8 heads gains 13 µs, config 5's
-// 65536 tokens on 16 heads 200 µs).
+// Single sequences at least this long on at most this many heads (their
+// 16-column scan fills at most half of a 256-CU device) run in segments of W
+// chunks: K1 of segment s+1 overlaps the scan of segment s on the CUs the
+// scan leaves idle, and the records live in a ring of 2W slots per head
+// instead of one slot per chunk. Each segment boundary costs the two streams'
+// event hand-offs (measured 10-20 µs), so segments hold about kSegmentChunks
+// chunks, at least two segments (65536 tokens on 16 heads, 1024 chunks: 8
+// segments 1473 µs, 6 1471, 4 1444, two of 47% / 53% 1516; 16384 tokens on 8
+// heads: 2 segments 314 µs, 4 324, 8 385).
 constexpr int kSplitMinTokens = 16384;
+constexpr int kSplitMaxHeads = 16;
+constexpr int kSegmentChunks = 256;
+
+bool windowed_shape(int T, int N, int H) { return N == 1 && T >= kSplitMinTokens && H <= kSplitMaxHeads; }
+
+int chunk_bound(int T) { return (T + BT - 1) / BT; }  // chunks of one sequence of T tokens
+
+int segment_count(int T) {
+    const int segs = (chunk_bound(T) + kSegmentChunks - 1) / kSegmentChunks;
+    return segs < 2 ? 2 : segs;
+}
+// The first segment runs its K1 alone on the device; with two segments it
+// holds 47% of the chunks (the best of 35-62% measured), otherwise its share.
+int first_segment(int T) {
+    const int nch = chunk_bound(T);
+    const int segs = segment_count(T);
+    return segs == 2 ? (nch * 47 + 50) / 100 : (nch + segs - 1) / segs;
+}
+// The longest segment: the ring holds two of them per head.
+int window_chunks(int T) {
+    const int nch = chunk_bound(T);
+    const int first = first_segment(T);
+    const int segs = segment_count(T);
+    return segs == 2 ? nch - first : first;
+}
+
+// The workspace a call needs: the ring of 2W slots for the segmented shape,
+// one slot per chunk otherwise.
+size_t required_bytes(int T, int N, int H) {
+    return windowed_shape(T, N, H) ? layout(T, 1, H, 2 * window_chunks(T)).total : layout(T, N, H).total;
+}
+
+// The largest window (segments run one after another, so a ring of W slots)
+// whose layout fits `bytes` for one sequence, or 0.
+int fit_window(int T, int H, size_t bytes) {
+    const Layout base = layout(T, 1, H, 0);
+    if (base.total > bytes) {
+        return 0;
+    }
+    const size_t per = static_cast<size_t>(kRecBytes) * H;
+    const size_t w = (bytes - base.total) / per;
+    const int cap = chunk_bound(T) > 0 ? chunk_bound(T) : 1;
+    return w > static_cast<size_t>(cap) ? cap : static_cast<int>(w);
+}
 
 }  // namespace chunk
 }  // namespace kda
@@ -1860,7 +1935,7 @@ extern "C" size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs
     if (num_tokens < 0 || num_seqs < 0 || num_heads <= 0 || head_dim != kda::chunk::DK) {
         return 0;
     }
-    return kda::chunk::layout(num_tokens, num_seqs, num_heads).total;
+    return kda::chunk::required_bytes(num_tokens, num_seqs, num_heads);
 }
 
 namespace kda {
@@ -1907,21 +1982,24 @@ int check_args(const KdaChunkArgs *args) {
 }
 
 // Enqueues the chunk kernels on `st` with `ws` (checked by the caller) as the
-// workspace. `allow_split` permits the two-segment form (which uses the
-// library's side stream).
-int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, bool allow_split) {
-    const Layout LY = layout(a.num_tokens, a.num_seqs, a.num_heads);
+// workspace. `win` = 0: one pass, a record slot per chunk. `win` > 0 (one
+// sequence only): segments of `win` chunks (the first of `first_seg`, when
+// given, at most `win`) with records in a ring of `ring` slots per head; with
+// `pipeline` (ring = 2 win) K1 of segment s+1 runs on the library's side
+// stream while segment s is scanned, otherwise (ring >= win) the segments run
+// one after another on `st`.
+int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, int ring, int win, bool pipeline, int first_seg = 0) {
     KdaChunkArgs kargs = a;
-    int *cs = reinterpret_cast<int *>(ws + LY.chunk_start);
     const int nrec = max_chunks(a.num_tokens, a.num_seqs);
-    const int64_t prep_blocks = static_cast<int64_t>(nrec) * a.num_heads;
     const int64_t pairs = static_cast<int64_t>(a.num_seqs) * a.num_heads;
     const int nt = scan_tiles(pairs, st);
     const int64_t blocks = scan_blocks(pairs, nt);
-    if (prep_blocks > 0x7fffffff || blocks > 0x7fffffff) {
+    if (static_cast<int64_t>(nrec) * a.num_heads > 0x7fffffff || blocks > 0x7fffffff) {
         return KDA_ERR_INVALID_ARGUMENT;
     }
     if (a.num_seqs > 1) {  // one sequence needs no chunk index (K1 and K2 derive it)
+        const Layout LY = layout(a.num_tokens, a.num_seqs, a.num_heads, ring);
+        int *cs = reinterpret_cast<int *>(ws + LY.chunk_start);
         void *params[] = {&kargs, &cs};
         if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_index_kernel), dim3(1), dim3(1024),
                             params, 0, st) != hipSuccess) {
@@ -1931,43 +2009,76 @@ int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, bool allow_split) {
     const void *prep = a.gate_mode == KDA_GATE_RAW
                            ? reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_RAW>)
                            : reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_LOG>);
-    auto launch_prep = [&](int seg, hipStream_t s) {
-        int nr = nrec;
-        int sg = seg;
-        void *params[] = {&kargs, &ws, &nr, &sg};
-        return hipLaunchKernel(prep, dim3(static_cast<unsigned>(prep_blocks)), dim3(kThreads),
-                               params, 0, s) == hipSuccess;
+    // K1 over chunks [lo, hi)
+    auto launch_prep = [&](int lo, int hi, hipStream_t s) {
+        if (hi <= lo) {
+            return true;
+        }
+        int rg = ring, l = lo, h = hi;
+        void *params[] = {&kargs, &ws, &rg, &l, &h};
+        return hipLaunchKernel(prep, dim3(static_cast<unsigned>(static_cast<int64_t>(hi - lo) * a.num_heads)),
+                               dim3(kThreads), params, 0, s) == hipSuccess;
     };
-    auto launch_scan = [&](int seg) {
+    // K2 over all chunks (seg false) or the segment [lo, hi)
+    auto launch_scan = [&](bool seg, int lo, int hi) {
         const char *cws = ws;
-        int sg = seg;
-        void *params[] = {&kargs, &cws, &sg};
-        return hipLaunchKernel(scan_kernel(nt, seg != 0), dim3(static_cast<unsigned>(blocks)),
-                               dim3(kScanThreads), params, 0, st) == hipSuccess;
+        int rg = ring, l = lo, h = hi;
+        void *params[] = {&kargs, &cws, &rg, &l, &h};
+        return hipLaunchKernel(scan_kernel(nt, seg), dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads),
+                               params, 0, st) == hipSuccess;
     };
+    if (win <= 0) {
+        return launch_prep(0, nrec, st) && launch_scan(false, 0, 0) ? KDA_OK : KDA_ERR_LAUNCH;
+    }
+    // one sequence; segments cover the chunks T tokens can hold (a shorter
+    // sequence leaves its trailing segments empty: their workgroups return).
+    // The first segment holds `first` chunks, the others `win`.
+    const int nch_max = chunk_bound(a.num_tokens);
+    const int first = first_seg > 0 ? first_seg : win;
+    const int nseg = nch_max <= first ? 1 : 1 + (nch_max - first + win - 1) / win;
+    auto seg_lo = [&](int s) { return s == 0 ? 0 : first + (s - 1) * win; };
+    auto seg_hi = [&](int s) { return first + s * win < nch_max ? first + s * win : nch_max; };
     SideStream side;
-    const bool split = allow_split && a.num_seqs == 1 && nt == 1 && a.num_tokens >= kSplitMinTokens &&
-                       pairs * 8 * 2 <= device_cus(st) && side_stream(st, side);
-    if (split) {
-        // st:    K1(seg 1) -> fork -> K2(seg 1) -> [wait join] -> K2(seg 2)
-        // side:                [wait fork] -> K1(seg 2) -> join
-        // (the side stream starts after K1 of the first segment, so its K1 runs
-        // on the CUs the first scan leaves idle). A side stream that another
-        // thread's graph capture has pulled in is not used.
+    if (pipeline && nt == 1 && ring >= 2 * win && side_stream(st, side)) {
+        // st:   K1(0) | [wait done1(s)] go(s) K2(s) ...
+        // side:        [wait go(s)] K1(s+1) done1(s+1) ...
+        // K1(s+1) is released together with the scan of segment s (go(s) is
+        // recorded just before it), never earlier: a scan workgroup needs a
+        // CU of its own, and K1 workgroups released ahead of the scan would
+        // fill every CU first. go(s) follows K2(s-1) on st, so the ring half
+        // K1(s+1) rewrites has been read. A side stream that another thread's
+        // graph capture has pulled in is not used.
         std::lock_guard<std::mutex> lock(*side.order);
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(side.stream, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
-            if (!launch_prep(1, st) || hipEventRecord(side.fork, st) != hipSuccess ||
-                hipStreamWaitEvent(side.stream, side.fork, 0) != hipSuccess ||
-                !launch_prep(2, side.stream) || hipEventRecord(side.join, side.stream) != hipSuccess ||
-                !launch_scan(1) || hipStreamWaitEvent(st, side.join, 0) != hipSuccess || !launch_scan(2)) {
+            if (!launch_prep(seg_lo(0), seg_hi(0), st)) {
                 return KDA_ERR_LAUNCH;
+            }
+            for (int s = 0; s < nseg; ++s) {
+                hipEvent_t go = side.done2[s & 1];
+                if (s >= 1 && hipStreamWaitEvent(st, side.done1[s & 1], 0) != hipSuccess) {
+                    return KDA_ERR_LAUNCH;
+                }
+                if (s + 1 < nseg &&
+                    (hipEventRecord(go, st) != hipSuccess || hipStreamWaitEvent(side.stream, go, 0) != hipSuccess ||
+                     !launch_prep(seg_lo(s + 1), seg_hi(s + 1), side.stream) ||
+                     hipEventRecord(side.done1[(s + 1) & 1], side.stream) != hipSuccess)) {
+                    return KDA_ERR_LAUNCH;
+                }
+                if (!launch_scan(true, seg_lo(s), seg_hi(s))) {
+                    return KDA_ERR_LAUNCH;
+                }
             }
             return KDA_OK;
         }
         (void)hipGetLastError();
     }
-    return launch_prep(0, st) && launch_scan(0) ? KDA_OK : KDA_ERR_LAUNCH;
+    for (int s = 0; s < nseg; ++s) {
+        if (!launch_prep(seg_lo(s), seg_hi(s), st) || !launch_scan(true, seg_lo(s), seg_hi(s))) {
+            return KDA_ERR_LAUNCH;
+        }
+    }
+    return KDA_OK;
 }
 
 // The no-allocation entry point's scratch: one array per device, held until
@@ -2020,11 +2131,28 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
         return rc;
     }
     const KdaChunkArgs &a = *args;
-    const Layout LY = layout(a.num_tokens, a.num_seqs, a.num_heads);
-    if (workspace == nullptr || workspace_bytes < LY.total || !aligned(workspace, 256)) {
+    if (workspace == nullptr || !aligned(workspace, 256)) {
         return KDA_ERR_WORKSPACE;
     }
-    return launch(a, static_cast<char *>(workspace), static_cast<hipStream_t>(stream), true);
+    char *ws = static_cast<char *>(workspace);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int T = a.num_tokens;
+    const int H = a.num_heads;
+    if (workspace_bytes >= required_bytes(T, a.num_seqs, H)) {
+        if (windowed_shape(T, a.num_seqs, H)) {
+            const int w = window_chunks(T);
+            return launch(a, ws, st, 2 * w, w, true, first_segment(T));
+        }
+        return launch(a, ws, st, max_chunks(T, a.num_seqs), 0, false);
+    }
+    // a smaller workspace: one sequence in segments that fit it
+    if (a.num_seqs == 1) {
+        const int w = fit_window(T, H, workspace_bytes);
+        if (w > 0) {
+            return launch(a, ws, st, w, w, false);
+        }
+    }
+    return KDA_ERR_WORKSPACE;
 }
 
 extern "C" int kda_chunk_launch_noalloc(const KdaChunkArgs *args, void *stream) {
@@ -2034,7 +2162,11 @@ extern "C" int kda_chunk_launch_noalloc(const KdaChunkArgs *args, void *stream) 
         return rc;
     }
     const KdaChunkArgs &a = *args;
-    if (layout(a.num_tokens, a.num_seqs, a.num_heads).total > KDA_NOALLOC_SCRATCH_BYTES) {
+    const int T = a.num_tokens;
+    const int H = a.num_heads;
+    const bool whole = layout(T, a.num_seqs, H).total <= KDA_NOALLOC_SCRATCH_BYTES;
+    const int w = whole || a.num_seqs != 1 ? 0 : fit_window(T, H, KDA_NOALLOC_SCRATCH_BYTES);
+    if (!whole && w == 0) {
         return KDA_ERR_TOO_LARGE;
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -2042,5 +2174,5 @@ extern "C" int kda_chunk_launch_noalloc(const KdaChunkArgs *args, void *stream) 
     if (ws == nullptr) {
         return KDA_ERR_LAUNCH;
     }
-    return launch(a, ws, st, false);
+    return whole ? launch(a, ws, st, max_chunks(T, a.num_seqs), 0, false) : launch(a, ws, st, w, w, false);
 }

@@ -177,10 +177,12 @@ typedef struct KdaChunkArgs {
     int32_t qk_l2norm;
 } KdaChunkArgs;
 
-/* Bytes of device scratch kda_chunk_launch needs for these arguments. An
- * upper bound that depends only on T, N, H and D (no device reads): the
- * chunk records, the tracking records and, when N == 1, the state carried
- * between the two scan segments of a long sequence. */
+/* Bytes of device scratch kda_chunk_launch needs to run these arguments at
+ * full speed. An upper bound that depends only on T, N, H and D (no device
+ * reads): the chunk records (one per possible chunk and head, or, for a
+ * single sequence of at least 16384 tokens on at most 16 heads, a ring of two
+ * scan segments' records per head), the tracking records and, when N == 1,
+ * the state carried between scan segments. */
 size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
                                  int32_t num_heads, int32_t head_dim);
 
@@ -193,10 +195,15 @@ size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
  * lower_bound >= -10.9, and for LOG gates g >= -10.9 per token. Beyond it
  * the exponents are clamped: outputs and states stay finite but inexact.
  * `workspace`
- * must hold kda_chunk_workspace_bytes(...) bytes of device memory, 256-byte
- * aligned; its contents need no initialization. A single long sequence on few
- * heads forks its second segment's preparation onto a library-owned stream
- * and joins it back on `stream` (event fork/join; graph-capture safe).
+ * must be 256-byte aligned device memory of kda_chunk_workspace_bytes(...)
+ * bytes; its contents need no initialization. A single sequence (N == 1)
+ * also runs with less: the scan then goes through windows of as many chunks
+ * as the workspace holds records for (at least one chunk per head, else
+ * KDA_ERR_WORKSPACE), each window prepared and then scanned on `stream`.
+ * With the full workspace, a single sequence of at least 16384 tokens on at
+ * most 16 heads runs in segments of about 256 chunks: each next segment is
+ * prepared on a library-owned stream while the current one is scanned, forked
+ * from and joined back on `stream` by events (graph-capture safe).
  * Alignment
  * (KDA_ERR_INVALID_ARGUMENT otherwise): state 16 bytes with strides in
  * multiples of 4 elements; q, k, v and out 8 bytes; gate 8 (RAW) or 16. */
@@ -211,14 +218,16 @@ int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). The workspace is a static device array of
  * KDA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; its address
- * on a device is resolved on the first call on that device. Arguments whose
- * kda_chunk_workspace_bytes exceed it return KDA_ERR_TOO_LARGE (at K = V =
- * 128 roughly 750 (chunk, head) pairs, e.g. T = 1024 tokens on 32 heads, or
- * T = 8192 on 5). Results are those of kda_chunk_launch on the same
- * arguments, always in the single-pass form (no second stream). Every call on
- * one GPU shares that GPU's array (its contents need no initialization, the
- * last call's are left behind): calls that overlap on one GPU -- concurrent
- * streams, or host threads -- race, and must be serialized by the caller. */
+ * on a device is resolved on the first call on that device. Several sequences
+ * whose records do not fit it (at K = V = 128 roughly 750 (chunk, head)
+ * pairs, e.g. 1024 tokens on 32 heads) return KDA_ERR_TOO_LARGE; a single
+ * sequence of any length runs in windows of the chunks it holds (the small-
+ * workspace form of kda_chunk_launch: about 750 / H chunks, 23 on 32 heads).
+ * Results are those of kda_chunk_launch on the same arguments; no second
+ * stream is used. Every call on one GPU shares that GPU's array (its
+ * contents need no initialization, the last call's are left behind): calls
+ * that overlap on one GPU -- concurrent streams, or host threads -- race, and
+ * must be serialized by the caller. */
 int kda_chunk_launch_noalloc(const KdaChunkArgs *args, void *stream);
 
 /* Human-readable text of a KdaStatus. */

@@ -146,27 +146,37 @@ def test_chunk_launch_alignment_checks_need_no_device(lib):
 
 def test_chunk_workspace_size_formula(lib):
     """kda_chunk_workspace_bytes is a host-only function of (T, N, H, D): the
-    chunk-start table, one 87 KiB record per possible (chunk, head), one
-    16.75 KiB tracking record per (sequence, head) and, for a single sequence,
-    one 64 KiB state per head carried between scan segments, each 256-byte
-    aligned (the sizes the integration notes quote for sizing a reusable
-    workspace)."""
+    chunk-start table, 87 KiB records, one 16.75 KiB tracking record per
+    (sequence, head) and, for a single sequence, one 64 KiB state per head
+    carried between scan segments, each 256-byte aligned (the sizes the
+    integration notes quote for sizing a reusable workspace). The records: one
+    per possible (chunk, head), except for a single sequence of at least 16384
+    tokens on at most 16 heads, which runs in S = max(2, ceil(chunks / 256))
+    segments (two: 47% and 53% of the chunks; more: W = ceil(chunks / S)
+    each) and needs a ring of two of the longest per head."""
     lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
     lib.kda_chunk_workspace_bytes.argtypes = [ctypes.c_int32] * 4
     rec, track = 89088, 17152
     assert rec == 87 * 1024 and track == 16.75 * 1024
-    for T, N, H in [(8192, 1, 32), (33814, 16, 32), (65536, 1, 16), (1, 1, 1), (0, 3, 2)]:
+    for T, N, H in [(8192, 1, 32), (33814, 16, 32), (65536, 1, 16), (65536, 1, 17), (16383, 1, 4),
+                    (16384, 1, 4), (100000, 1, 8), (1, 1, 1), (0, 3, 2)]:
         header = ((N + 1) * 4 + 255) // 256 * 256
-        max_chunks = (T + 63) // 64 + N
-        expected = header + rec * max_chunks * H + track * N * H + (65536 * H if N == 1 else 0)
+        chunks = (T + 63) // 64
+        slots = chunks + N
+        if N == 1 and T >= 16384 and H <= 16:
+            segs = max(2, (chunks + 255) // 256)
+            first = (chunks * 47 + 50) // 100 if segs == 2 else (chunks + segs - 1) // segs
+            slots = 2 * (chunks - first if segs == 2 else first)
+        expected = header + rec * slots * H + track * N * H + (65536 * H if N == 1 else 0)
         assert lib.kda_chunk_workspace_bytes(T, N, H, 128) == expected, (T, N, H)
 
 
 def test_noalloc_rejects_what_its_scratch_cannot_hold(lib):
     """kda_chunk_launch_noalloc checks the arguments, then the size against its
-    static scratch, before any HIP call: a null block is invalid and a
-    prefill bigger than KDA_NOALLOC_SCRATCH_BYTES is refused with
-    KDA_ERR_TOO_LARGE (the addresses are never dereferenced)."""
+    static scratch, before any HIP call: a null block is invalid and a batch
+    of sequences bigger than KDA_NOALLOC_SCRATCH_BYTES is refused with
+    KDA_ERR_TOO_LARGE (the addresses are never dereferenced; a single
+    sequence that large runs in segments instead, a GPU test)."""
     lib.kda_chunk_launch_noalloc.restype = ctypes.c_int
     lib.kda_chunk_launch_noalloc.argtypes = [ctypes.POINTER(_ChunkArgs), ctypes.c_void_p]
     lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
@@ -178,10 +188,11 @@ def test_noalloc_rejects_what_its_scratch_cannot_hold(lib):
     assert lib.kda_chunk_launch_noalloc(None, None) == 1
     base = 1 << 20
     T = 8192
-    assert lib.kda_chunk_workspace_bytes(T, 1, 32, 128) > limit
+    # two sequences (only a single one can run in segments of the scratch)
+    assert lib.kda_chunk_workspace_bytes(T, 2, 32, 128) > limit
     a = _ChunkArgs(q=base, k=base, v=base, gate=base, beta=base, state=base,
                    state_stride_slot=32 * 128 * 128, state_stride_head=128 * 128, num_slots=4,
-                   state_indices=base, cu_seqlens=base, out=base, scale=1.0, num_seqs=1,
+                   state_indices=base, cu_seqlens=base, out=base, scale=1.0, num_seqs=2,
                    num_tokens=T, num_heads=32, head_dim=128, qk_dtype=0, v_dtype=0, gate_mode=1)
     assert lib.kda_chunk_launch_noalloc(ctypes.byref(a), None) == 5  # KDA_ERR_TOO_LARGE
     assert b"noalloc" in lib.kda_status_string(5)

@@ -361,11 +361,12 @@ def test_chunk_c_abi_launch_direct(gpu_ops):
         assert torch.equal(out, out_op) and torch.equal(pool, pool_op)
 
 
-# A single sequence of at least 16384 tokens whose scan leaves half the CUs
-# idle (heads x 16 <= CUs) runs in two segments, the first ~47% of its chunks
-# and the rest, with the second segment's prepare kernel on a second stream;
-# the state between them goes through the workspace. 256 chunks split at 120.
-_SPLIT = 120 * 64
+# A single sequence of at least 16384 tokens on at most 16 heads runs in
+# segments (two here: 120 and 136 of its 256 chunks), each segment's prepare
+# kernel on a second stream under the previous segment's scan, the records in
+# a ring of two segments' slots and the state between the segments in the
+# workspace; segments past a shorter sequence's end do nothing.
+_SEG = 120 * 64
 _T_SPLIT = 16384
 
 
@@ -374,11 +375,12 @@ _T_SPLIT = 16384
     ("zero slot", (0, _T_SPLIT), 0, None),
     ("offset and ragged", (37, _T_SPLIT - 42), 2, None),
     ("short sequence", (5, 100), 1, None),
+    ("one segment exactly", (0, _SEG), 1, None),
     ("track at 0", (0, _T_SPLIT), 1, 0),
     ("track in first segment", (0, _T_SPLIT), 1, 1000),
-    ("track at split", (0, _T_SPLIT), 1, _SPLIT),
-    ("track after split", (0, _T_SPLIT), 1, _SPLIT + 1),
-    ("track in second segment", (0, _T_SPLIT), 0, 14000),
+    ("track at a segment end", (0, _T_SPLIT), 1, _SEG),
+    ("track after a segment end", (0, _T_SPLIT), 1, _SEG + 1),
+    ("track in a later segment", (0, _T_SPLIT), 0, 14000),
     ("track at end", (0, _T_SPLIT), 1, _T_SPLIT),
 ])
 def test_chunk_two_segment_path(gpu_ops, label, bounds, slot, track):

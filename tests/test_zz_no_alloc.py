@@ -2,11 +2,12 @@
 
 The no-allocation entry point runs the chunk kernels on the library's static
 device scratch instead of a caller workspace. On the same arguments its
-outputs and pool must equal kda_chunk_launch's bit for bit (same kernels, one
-pass; both calls here stay below the two-segment length), on two calls in a
-row, the second smaller than the first (the scratch keeps the first call's
-contents, which must not leak into the second). A call that needs more
-scratch than the array holds is refused before anything is written.
+outputs and pool must equal kda_chunk_launch's bit for bit (same kernels), on
+two calls in a row, the second smaller than the first (the scratch keeps the
+first call's contents, which must not leak into the second). A single
+sequence too long for the scratch runs in segments that fit it (the state
+carried between them exactly, so still bit for bit); a batch of sequences too
+large for it is refused before anything is written.
 """
 
 import ctypes
@@ -80,12 +81,40 @@ def test_noalloc_matches_workspace_launch_twice():
         assert torch.isfinite(out_na.float()).all()
 
 
-def test_noalloc_refuses_oversized_call_untouched():
-    """A call beyond the static scratch returns KDA_ERR_TOO_LARGE and writes
-    nothing."""
+def test_noalloc_long_sequence_runs_in_segments():
+    """One sequence whose records exceed the scratch (8192 tokens on 32 heads,
+    ~370 MB in one pass) runs in segments of the scratch's size: outputs,
+    the updated slot and a prefix tracked in the middle of a segment equal
+    the one-pass workspace launch bit for bit."""
     lib = _lib()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    case = C.prepared_case(32, (2048,), slots=2, indices=[1], seed=73)
+    case = C.prepared_case(32, (8192,), slots=4, indices=[2], seed=74)
+    T, H, D = case.q.shape[1:]
+    nbytes = lib.kda_chunk_workspace_bytes(T, 1, H, D)
+    assert nbytes > (64 << 20)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    a_ref, out_ref, pool_ref, keep_ref = _prepare(case)
+    a_na, out_na, pool_na, keep_na = _prepare(case)
+    tr = torch.tensor([3], dtype=torch.int32, device=DEV)
+    tl = torch.tensor([4100], dtype=torch.int32, device=DEV)
+    for a in (a_ref, a_na):
+        a.track_indices = tr.data_ptr()
+        a.track_lens = tl.data_ptr()
+    assert lib.kda_chunk_launch(ctypes.byref(a_ref), ctypes.c_void_p(ws.data_ptr()),
+                                ctypes.c_size_t(nbytes), stream) == 0
+    assert lib.kda_chunk_launch_noalloc(ctypes.byref(a_na), stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out_na, out_ref), "outputs differ"
+    assert torch.equal(pool_na, pool_ref), "pools differ"
+    assert not torch.equal(pool_na[3], C.to_dev(case.pool, DEV)[3]), "the tracked slot was not written"
+
+
+def test_noalloc_refuses_oversized_call_untouched():
+    """A batch of sequences beyond the static scratch (only a single sequence
+    can run in segments) returns KDA_ERR_TOO_LARGE and writes nothing."""
+    lib = _lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    case = C.prepared_case(32, (1024, 1024), slots=3, indices=[1, 2], seed=73)
     a, out, pool, keep = _prepare(case)
     before = pool.clone()
     assert lib.kda_chunk_launch_noalloc(ctypes.byref(a), stream) == 5
