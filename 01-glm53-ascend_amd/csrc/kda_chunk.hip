@@ -1107,12 +1107,12 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 // barriers per chunk j: B1(j) after S_j is published, B2(j) after vnew_j is.
 //   chain waves 0-3   own S rows [32c, 32c+32) x CW columns (fp32, registers)
 //                     and run the recurrence: publish S_j, vnew_j = u - w S_j,
-//                     publish vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j,
-//                     then Aqk vnew_j for output rows [16c, 16c+16);
+//                     publish vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j;
 //   output waves 4-7  own token rows [16o, 16o+16): (q e^G) S_j between B2(j)
-//                     and B1(j+1), then o_j = that + Aqk vnew_j and its store
-//                     between B1(j+1) and B2(j+1); they load their q e^G
-//                     fragments themselves, a chunk ahead;
+//                     and B1(j+1), Aqk vnew_j between B1(j+1) and B2(j+1)
+//                     (Aqk from the stage, vnew_j from its LDS hand-over),
+//                     then o_j = the sum and its store after B2(j+1); they
+//                     load their q e^G fragments themselves, a chunk ahead;
 //   loader waves 8-11 copy the chain's operands of chunk j+1 (w, kd^T, Aqk,
 //                     this group's u, e^(G_last), the scales), loaded into
 //                     their registers after B2(j-2), into the LDS stage of
@@ -1120,9 +1120,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 //                     that stage's previous chunk j-1 finished before B1(j)),
 //                     then issue the loads of chunk j+3. The recurrence never
 //                     waits to issue a global load.
-// S_j, vnew_j, the Aqk hand-over and the stage are indexed by j's parity; a
-// buffer of parity j&1 is rewritten only after B1(j+1) or later, when its
-// chunk-j readers are done. One barrier B0 before the first chunk publishes
+// S_j, vnew_j and the stage are indexed by j's parity; a buffer of parity
+// j&1 is rewritten only after B1(j+1) or later, when its chunk-j readers are
+// done (the stage after B2(j+1): the output waves read its Aqk until then). One barrier B0 before the first chunk publishes
 // the first stage; one after the last chunk covers the last hand-over.
 //
 // S_j is published as fp16 scaled per 32-row slice (the state itself stays
@@ -1171,7 +1171,6 @@ struct ScanShared {
     char stg[2][Stage<NT>::kFrags * kFrag];  // chain operands by parity, fragments in lane order
     u32x4 sbuf[2][4][NT][64];                // S_j as fp16 B fragments: [parity][slice][tile][lane]
     u32x4 vbuf[2][2][2][NT][64];             // vnew_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
-    f32x4 obuf[2][4][NT][64];                // Aqk vnew_j rows [16c, 16c+16) from chain wave c
     float sscale[2][4];                      // 2^-shift of each S_j slice in sbuf
     float smax[2][4];                        // max |S_j| of each slice
     uint32_t otile[4][16][8 * NT];           // per output wave: 16 rows x CW bf16 columns
@@ -1407,10 +1406,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             const float inv_v = ldexpf(1.f, -sv);
             const float fw[4] = {ob.wsc.x * ss.x, ob.wsc.y * ss.y, ob.wsc.z * ss.z, ob.wsc.w * ss.w};
             f16x8 Kd[2][2];
-            f16x8 Aq[2];
             f32x4 gl[2];
             float2 kdsc;
-            float aqsc;
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
                 f32x4 acc[4];
@@ -1426,15 +1423,11 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                             Kd[tt][s] = stage_frag(st, kStKd + (2 * wr + tt) * 2 + s, lane);
                         }
                     }
-                    // Aqk rows [16wr, 16wr+16) meet tokens >= 32 only for wr >= 2
-                    Aq[0] = stage_frag(st, kStAq + aq_frag(wr, 0), lane);
-                    Aq[1] = stage_frag(st, kStAq + aq_frag(wr, wr >= 2 ? 1 : 0), lane);
 #pragma unroll
                     for (int tt = 0; tt < 2; ++tt) {
                         gl[tt] = reinterpret_cast<const f32x4 *>(st + St::kMisc)[4 * (2 * wr + tt) + gq];
                     }
                     kdsc = *reinterpret_cast<const float2 *>(sc + kScKd + 2 * wr);
-                    aqsc = sc[kScAq + wr];
                 }
                 float v[4];
 #pragma unroll
@@ -1507,14 +1500,6 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                         S[tt][ct][i] = S[tt][ct][i] * gl[tt][i] + su[i] * f;
                     }
                 }
-                // Aqk vnew_j rows [16wr, 16wr+16), for output wave wr
-                f32x4 acc2 = mfma(Aq[0], vh[0], z4);
-                acc2 = mfma(Aq[0], vl[0], acc2);
-                if (wr >= 2) {
-                    acc2 = mfma(Aq[1], vh[1], acc2);
-                    acc2 = mfma(Aq[1], vl[1], acc2);
-                }
-                sm.obuf[p][wr][ct][lane] = acc2 * (aqsc * inv_v);
             }
             if (track_slot > 0 && rr == len) {
                 store_S(track_slot, S);
@@ -1526,7 +1511,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             step(j);
         }
         if (j1 > j0) {
-            lds_barrier();  // B1(j1): the last Aqk vnew is in obuf
+            lds_barrier();  // B1(j1)
         }
         if (!last) {
 #pragma unroll
@@ -1543,18 +1528,48 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     } else if (w < 8) {
         // ------------------------------- output waves ------------------------------
         f32x4 P[NT];  // (q e^G) S of the chunk whose output is pending
+        f32x4 A[NT];  // Aqk vnew of that chunk
 #pragma unroll
         for (int ct = 0; ct < NT; ++ct) {
             P[ct] = z4;
+            A[ct] = z4;
         }
-        // o_j = P + Aqk vnew_j; rows t < len of chunk j are stored, transposed
-        // through this wave's LDS tile so each lane writes CW/4 consecutive
-        // columns of one row (nontemporal stores).
+        // A = Aqk vnew_j for rows [16wr, 16wr+16): Aqk from chunk j's stage
+        // (rewritten only after B2(j+1)), vnew_j hi + lo from vbuf (published
+        // before B2(j), rewritten after B1(j+2)), scaled as the chain scaled it.
+        auto aqk_vnew = [&](int j) {
+            const int p = j & 1;
+            const char *st = sm.stg[p];
+            const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
+            const float4 um = *reinterpret_cast<const float4 *>(sc + kScUmax);
+            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScWl1);
+            const float4 sx = *reinterpret_cast<const float4 *>(&sm.smax[p][0]);
+            const int sv = f16_shift(fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w)) +
+                                     fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w)) *
+                                         fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
+            const float f = sc[kScAq + wr] * ldexpf(1.f, -sv);
+            // rows [16wr, 16wr+16) meet tokens >= 32 only for wr >= 2
+            const f16x8 aq0 = stage_frag(st, kStAq + aq_frag(wr, 0), lane);
+            const f16x8 aq1 = stage_frag(st, kStAq + aq_frag(wr, wr >= 2 ? 1 : 0), lane);
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) {
+                f32x4 acc = mfma(aq0, as_f16x8(sm.vbuf[p][0][0][ct][lane]), z4);
+                acc = mfma(aq0, as_f16x8(sm.vbuf[p][0][1][ct][lane]), acc);
+                if (wr >= 2) {
+                    acc = mfma(aq1, as_f16x8(sm.vbuf[p][1][0][ct][lane]), acc);
+                    acc = mfma(aq1, as_f16x8(sm.vbuf[p][1][1][ct][lane]), acc);
+                }
+                A[ct] = acc * f;
+            }
+        };
+        // o_j = P + A; rows t < len of chunk j are stored, transposed through
+        // this wave's LDS tile so each lane writes CW/4 consecutive columns of
+        // one row (nontemporal stores).
         auto finish = [&](int j) {
             uint16_t *ot = reinterpret_cast<uint16_t *>(&sm.otile[wr][0][0]);
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                const f32x4 acc = P[ct] + sm.obuf[j & 1][wr][ct][lane];
+                const f32x4 acc = P[ct] + A[ct];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     ot[(4 * gq + i) * CW + 16 * ct + r] = f32_to_bf16(acc[i]);
@@ -1601,14 +1616,17 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
             op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 4 * (kScQg + 4 * wr));
         };
-        // Iteration j: [B1(j)] load chunk j+1 into `other`, [B2(j)] finish
-        // chunk j-1 (its Aqk vnew is in obuf since B2(j-1) and is rewritten
-        // only after B2(j+1)), then P = (q e^G) S_j from `cur`: fp16 q e^G
-        // against fp16 S_j, one product per slice, then scaled.
+        // Iteration j: [B1(j)] load chunk j+1 into `other` and form A of
+        // chunk j-1, [B2(j)] finish chunk j-1, then P = (q e^G) S_j from
+        // `cur`: fp16 q e^G against fp16 S_j, one product per slice, then
+        // scaled.
         auto iter = [&](const OpsO &cur, OpsO &other, int j) {
             const int p = j & 1;
             lds_barrier();  // B1(j)
             load_out(other, j + 1);
+            if (j > j0) {
+                aqk_vnew(j - 1);
+            }
             lds_barrier();  // B2(j)
             if (j > j0) {
                 finish(j - 1);
@@ -1646,7 +1664,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             iter(opB, opA, j + 1);
         }
         if (j1 > j0) {
-            lds_barrier();  // B1(j1): the chain's last Aqk vnew is in obuf
+            lds_barrier();  // B1(j1)
+            aqk_vnew(j1 - 1);
             finish(j1 - 1);
         }
     } else {
