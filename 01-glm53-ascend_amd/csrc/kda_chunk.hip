@@ -12,6 +12,9 @@
 //     S  <- e^(G_last) * S + (e^(G_last - G) * k)^T vnew
 // Sequences of any length are accepted: a short last chunk is zero-padded
 // (k = q = v = 0, g = 0, beta = 0), which leaves every equation above exact.
+// Since vnew = T (v - (e^G k) S), this file computes, with y = v - (e^G k) S,
+//     o = (q e^G) S + (Aqk T) y,   S <- e^(G_last) * S + (T^T kd)^T y
+// (kd = e^(G_last - G) * k): u, w and vnew are never formed.
 //
 // MI355X structure (three launches, one stream, no host synchronization):
 //   K0 chunk_index_kernel   prefix sums of ceil(len/64) per sequence, so the
@@ -22,24 +25,25 @@
 //                           factor spans more than 8 tokens of decay, all
 //                           column factors of earlier blocks e^(<=0)), the
 //                           blocked triangular inverse in
-//                           fp32, w and u on MFMA; writes the scan's operands as
-//                           ready MFMA fragments;
+//                           fp32, T^T kd and Aqk T on MFMA; writes the scan's
+//                           operands as ready MFMA fragments;
 //   K2 chunk_scan_kernel    one workgroup per (sequence, head, 16 or 32 value
 //                           columns), the serial chunk recurrence: four chain
-//                           waves carry S (fp32, registers) and vnew, four
+//                           waves carry S (fp32, registers) and y, four
 //                           output waves compute o one phase behind, four
-//                           loader waves stage the chain's operands in LDS;
-//                           S and vnew are exchanged through LDS.
+//                           loader waves stage the chain's operands and v in
+//                           LDS; S and y are exchanged through LDS.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16 / _f16 with fp32 accumulation. Inside K1,
 // operands whose rounding would break the tolerance contract are carried as
 // bf16 hi + lo pairs (x = hi + lo to ~2^-17) and multiplied in two or three
-// passes: u = T v (T split, v exact) and Aqk (q split, then k split); Akk
-// runs single-pass. The record the scan reads holds every matrix operand as
-// fp16 (11-bit significands) with a power-of-two scale per fragment or row
-// tile: w, q e^G, kd^T and Aqk. The scan meets them with S_j as fp16 (scaled
-// per 32-row slice; S itself stays fp32) for w S and (q e^G) S, and with
-// vnew as fp16 hi + lo (~2^-22) for kd^T vnew and Aqk vnew.
+// passes: Aqk (q split, then k split); Akk runs single-pass; T^T kd and
+// Aqk T take T, kd and Aqk as fp16 hi + lo pairs (~2^-22) in three passes.
+// The record the scan reads holds every matrix operand as fp16 (11-bit
+// significands) with a power-of-two scale per fragment or row tile: e^G k,
+// q e^G, (T^T kd)^T and Aqk T. The scan meets them with S_j as fp16 (scaled
+// per 32-row slice; S itself stays fp32) for (e^G k) S and (q e^G) S, and
+// with y as fp16 hi + lo (~2^-22) for (T^T kd)^T y and (Aqk T) y.
 //
 // Fragment conventions (lane l, r = l % 16, g = l / 16), shared by A and B so
 // that C-layout accumulators can be fed back as B operands without moving
@@ -74,31 +78,32 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Workspace record of one (chunk, head), in 16-byte-per-lane fragments
-// (a fragment is 64 lanes x 16 B = 1 KiB).
+// (a fragment is 64 lanes x 16 B = 1 KiB). With T = (I + diag(beta) Akk)^-1
+// diag(beta) the chunk's UT transform, the scan forms y = v - (e^G k) S
+// from the input v and never vnew = T y itself: the record holds the
+// operands of y, of the state update (T^T kd)^T y and of the output
+// (q e^G) S + (Aqk T) y. Every matrix operand is fp16 with a power-of-two
+// scale (held in the scale block); the first 38 fragments are the chain's
+// operands that every column group of a (sequence, head) reads whole, in
+// the order the scan stages them.
 constexpr int kFrag = 1024;
-// Every matrix operand is fp16 with a power-of-two scale (held in the
-// scale block); the first 38 fragments are the chain's operands that every
-// column group of a (sequence, head) reads whole, in the order the scan
-// stages them.
-constexpr int kOffW = 0;                          // w fp16: A (mt 0..3, s 0..3)
-constexpr int kOffKd = kOffW + 16 * kFrag;        // kd^T fp16: A (mk 0..7, s 0..1)
-constexpr int kOffAq = kOffKd + 16 * kFrag;       // Aqk fp16: A (mt, s), see aq_frag
+constexpr int kOffKe = 0;                         // e^G k fp16: A (mt 0..3, s 0..3)
+constexpr int kOffKd = kOffKe + 16 * kFrag;       // (T^T kd)^T fp16: A (mk 0..7, s 0..1)
+constexpr int kOffAq = kOffKd + 16 * kFrag;       // Aqk T fp16: A (mt, s), see aq_frag
 constexpr int kOffQg = kOffAq + 6 * kFrag;        // q e^G fp16: A (mt, s)
-constexpr int kOffU = kOffQg + 16 * kFrag;        // u fp32: C (mt 0..3, vt 0..7)
-constexpr int kOffGl = kOffU + 32 * kFrag;        // e^(G_last) fp32 [128]
+constexpr int kOffGl = kOffQg + 16 * kFrag;       // e^(G_last) fp32 [128]
 constexpr int kOffSc = kOffGl + DK * 4;           // fp32 scale block [128], indices below
-constexpr int kRecBytes = kOffSc + 512;           // 89088
-// Scale block: 2^-shift of each fp16 fragment group, and the two bounds the
-// scan derives vnew's scale from.
-constexpr int kScW = 0;      // [16] w fragment (mt, s): mt * 4 + s
+constexpr int kRecBytes = kOffSc + 512;           // 56320
+// Scale block: 2^-shift of each fp16 fragment group, and the bound the scan
+// derives y's scale from (|y| <= max|v| + kel1 max|S|).
+constexpr int kScKe = 0;     // [16] e^G k fragment (mt, s): mt * 4 + s (equal over s)
 constexpr int kScQg = 16;    // [16] q e^G fragment (mt, s)
-constexpr int kScKd = 32;    // [8]  kd^T row tile mk (both token slices)
-constexpr int kScAq = 40;    // [4]  Aqk row tile mt (both token slices)
-constexpr int kScUmax = 44;  // [4]  max |u| over row tile mt (all 128 columns)
-constexpr int kScWl1 = 48;   // [4]  max over the rows of tile mt of sum_k |w[t][k]|
+constexpr int kScKd = 32;    // [8]  (T^T kd)^T row tile mk (both token slices)
+constexpr int kScAq = 40;    // [4]  Aqk T row tile mt (both token slices)
+constexpr int kScKel1 = 48;  // [4]  max over the rows t of tile mt of sum_k |(e^G k)[t][k]|
 // Track record of one (sequence, head): operands of the state after r < len
 // tokens of the chunk holding the tracked position.
-constexpr int kTrOffKd = 0;                       // fp16, scaled per row tile mk
+constexpr int kTrOffKd = 0;                       // (T^T kd_r)^T fp16, scaled per row tile mk
 constexpr int kTrOffGl = kTrOffKd + 16 * kFrag;
 constexpr int kTrOffSc = kTrOffGl + DK * 4;       // fp32 [8]
 constexpr int kTrBytes = kTrOffSc + 256;          // 17152
@@ -220,11 +225,11 @@ __device__ __forceinline__ float wave_max(float x) {
     return fmaxf(a, b);
 }
 
-// One wave stores NF (1 or 2) consecutive fp16 fragments with one shared
-// scale, and writes the inverse scale to *sc.
+// One wave stores NF consecutive fp16 fragments with one shared scale, and
+// writes the inverse scale to sc[0 .. nsc).
 template <int NF>
 __device__ __forceinline__ void store_frags_f16(char *base, int off, int idx, float *sc, int lane,
-                                                const float (&x)[NF][8]) {
+                                                const float (&x)[NF][8], int nsc = 1) {
     float m = 0.f;
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -238,8 +243,8 @@ __device__ __forceinline__ void store_frags_f16(char *base, int off, int idx, fl
     for (int f = 0; f < NF; ++f) {
         reinterpret_cast<u32x4 *>(base + off)[(idx + f) * 64 + lane] = as_u32x4(to_f16x8(x[f], sh));
     }
-    if (lane == 0) {
-        *sc = ldexpf(1.f, -sh);
+    if (lane < nsc) {
+        sc[lane] = ldexpf(1.f, -sh);
     }
 }
 __device__ __forceinline__ void store_frag_f16(char *rec, int off, int idx, int sc_idx, int lane,
@@ -375,15 +380,13 @@ struct PrepShared {
             float qss[2][BT];       // sum of q^2 over each channel half, per row (S1-S3)
         } early;
         struct {
-            float X[BT][kPadX];      // (I + L)^-1, then T = X diag(beta) (S5-S6)
+            float X[BT][kPadX];  // (I + L)^-1; T = X diag(beta) (S5-S6)
             // Strict upper triangle: L^T, LT[j][i] = beta_i Akk[i][j] (j < i).
             // Lower triangle with the diagonal: Aqk[i][j] (j <= i).
             float LT[BT][kPadX];
-            uint16_t KE[BT][kPadT];  // e^G k as bf16, row-major (S4-S6)
+            u32x4 TT[4][2][2][64];  // T^T A fragments (row tile, token slice, hi / lo) (S6)
+            float ttinv[4];         // their 2^-shift per row tile
         } mid;
-        struct {
-            uint16_t V[BT][kPadT];  // v, bf16 bits, row-major (S6, over the dead X and LT)
-        } late;
     } u;
     float beta[BT];
     float rnk[BT];        // k row scale (1 / norm, or 1)
@@ -736,7 +739,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
     }
 
-    // ---- S4: kd^T fragments, e^(G_last), tracking operands, e^G k ----------
+    // ---- S4: kd fragments (kept for S6), e^(G_last), tracking operands, e^G k
+    // fragments of the record --------------------------------------------------
     // k[t][16mk + r] rnk[t] for the rows t = 32s + kperm(gq, e) of a kd^T
     // fragment: k by transposing reads, the row scales as two float4 reads.
     auto kd_rows = [&](int s, int mk, float (&kr)[8]) {
@@ -748,6 +752,30 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         for (int e = 0; e < 8; ++e) {
             kr[e] = static_cast<float>(kb[e]) * rn[e];
         }
+    };
+    // kd[t][16mk + r] = k_t e^(G_last - G_t) for the rows t = 32s + kperm(gq, e)
+    // (B fragments of T^T kd, mk = 2 wave + tt), fp16 hi + lo with one
+    // power-of-two scale per mk; S6 uses them from registers.
+    u32x4 kdh[2][2], kdl[2][2];
+    float kdinv[2];
+    auto to_frags = [&](const float (&x)[2][8], u32x4 (&fh)[2], u32x4 (&fl)[2], float &inv) {
+        float m = 0.f;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                m = fmaxf(m, fabsf(x[s][e]));
+            }
+        }
+        const int sh = f16_shift(wave_max(m));
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            f16x8 hi, lo;
+            split_f16x8(x[s], sh, hi, lo);
+            fh[s] = as_u32x4(hi);
+            fl[s] = as_u32x4(lo);
+        }
+        inv = ldexpf(1.f, -sh);
     };
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -765,19 +793,26 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 x[s][e] = kr[e] * ex2(gl - sm.u.early.G[t][k]);
             }
         }
-        store_frags_f16<2>(rec, kOffKd, mk * 2, reinterpret_cast<float *>(rec + kOffSc) + kScKd + mk, lane, x);
+        to_frags(x, kdh[tt], kdl[tt], kdinv[tt]);
     }
     if (tid < DK) {
         reinterpret_cast<float *>(rec + kOffGl)[tid] = ex2(sm.u.early.G[BT - 1][tid]);
     }
     // The tracked prefix inside this chunk (0 < rr < len): its state is
-    // e^(G_{rr-1}) S + (e^(G_{rr-1} - G_t) k_t)_{t<rr}^T vnew.
+    // e^(G_{rr-1}) S + (e^(G_{rr-1} - G_t) k_t)_{t<rr}^T vnew, i.e.
+    // e^(G_{rr-1}) S + (T^T kd_r)^T y with kd_r that prefix's kd; its kd
+    // fragments wait in registers for S6, like the chunk's.
+    bool tracked = false;
+    char *tr = nullptr;
+    u32x4 kth[2][2], ktl[2][2];
+    float ktinv[2] = {0.f, 0.f};
     if (a.track_indices != nullptr) {
         const int ts = a.track_indices[n];
         const int tl = a.track_lens[n];
         const int rr = tl - BT * jc;
         if (ts > 0 && static_cast<int64_t>(ts) < a.num_slots && rr > 0 && rr < len) {
-            char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
+            tracked = true;
+            tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 const int mk = 2 * wave + tt;
@@ -794,46 +829,42 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                         x[s][e] = t < rr ? kr[e] * ex2(gr - sm.u.early.G[t][k]) : 0.f;
                     }
                 }
-                store_frags_f16<2>(tr, kTrOffKd, mk * 2, reinterpret_cast<float *>(tr + kTrOffSc) + mk, lane, x);
+                to_frags(x, kth[tt], ktl[tt], ktinv[tt]);
             }
             if (tid < DK) {
                 reinterpret_cast<float *>(tr + kTrOffGl)[tid] = ex2(sm.u.early.G[rr - 1][tid]);
             }
         }
     }
-    // e^G k rows rg + 8i, columns 4kc..4kc+3, as bf16 (written after the barrier)
-    uint2 kep[8];
+    // e^G k fragments (A, row tile mt = wave, channel slices 0..3) for the
+    // scan's (e^G k) S, one scale per row tile; kel1 = max over the tile's
+    // rows of sum_k |e^G k| bounds that product with max |S|.
+    {
+        const int row = 16 * wave + r;
+        const float rk = sm.rnk[row];
+        float x[4][8];
+        float l1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int t = rg + 8 * i;
-        const uint2 k2 = *reinterpret_cast<const uint2 *>(&sm.u.early.K[t][4 * kc]);
-        const float4 g4 = *reinterpret_cast<const float4 *>(&sm.u.early.G[t][4 * kc]);
-        const float rn = sm.rnk[t];
-        kep[i].x = pack_bf16x2(__uint_as_float(k2.x << 16) * rn * ex2(g4.x),
-                               __uint_as_float(k2.x & 0xffff0000u) * rn * ex2(g4.y));
-        kep[i].y = pack_bf16x2(__uint_as_float(k2.y << 16) * rn * ex2(g4.z),
-                               __uint_as_float(k2.y & 0xffff0000u) * rn * ex2(g4.w));
+        for (int s = 0; s < 4; ++s) {
+            float kk[8], gg[8];
+            load_k8(row, s, kk);
+            load_g8(row, s, gg);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x[s][e] = kk[e] * rk * ex2(gg[e]);
+                l1 += fabsf(x[s][e]);
+            }
+        }
+        l1 += __shfl_xor(l1, 16);
+        l1 += __shfl_xor(l1, 32);
+        l1 = wave_max(l1);
+        float *sc = reinterpret_cast<float *>(rec + kOffSc);
+        store_frags_f16<4>(rec, kOffKe, wave * 4, sc + kScKe + wave * 4, lane, x, 4);
+        if (lane == 0) {
+            sc[kScKel1 + wave] = l1;
+        }
     }
     lds_barrier();  // G and K are dead from here on
-    // v rows rg + 8i, columns 4kc..4kc+3, loaded now (their latency hides
-    // behind S5) and written to LDS in S6, over X and LT
-    uint2 vraw[8];
-    {
-        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int t = rg + 8 * i;
-            const int tc = t < len ? t : len - 1;
-            vraw[i] = *reinterpret_cast<const uint2 *>(
-                vp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + 4 * kc);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t keep = keep_mask(rg + 8 * i < len);
-            vraw[i].x &= keep;
-            vraw[i].y &= keep;
-        }
-    }
     // S3's two channel halves meet in LT, which lies over the dead G: half
     // sh = 1 stores its partial products, then half sh = 0 adds its own and
     // applies beta. Every LT element is written: block (J, I), J < I, holds
@@ -861,11 +892,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 }
             }
         }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int t = rg + 8 * i;
-        *reinterpret_cast<uint2 *>(&sm.u.mid.KE[t][4 * kc]) = kep[i];
     }
     // X: the six upper 16x16 blocks (I, J > I) zero, one float4 per store
     for (int f = tid; f < 6 * 64; f += kThreads) {
@@ -909,34 +935,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         }
     }
     lds_barrier();
-    {
-        // Aqk fragments (mt = wave, s): rows 16 wave + r, zero above the diagonal
-        // (rows < 32 meet only slice 0; fragments aq_frag(wave, 0..1) are
-        // consecutive), one scale per row tile
-        const int row = 16 * wave + r;
-        float x[2][8];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 4 * gq]);
-            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 16 + 4 * gq]);
-            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                x[s][e] = 32 * s + kperm(gq, e) <= row ? xv[e] : 0.f;
-            }
-        }
-        float *asc = reinterpret_cast<float *>(rec + kOffSc) + kScAq + wave;
-        if (wave < 2) {
-            float x1[1][8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                x1[0][e] = x[0][e];
-            }
-            store_frags_f16<1>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x1);
-        } else {
-            store_frags_f16<2>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x);
-        }
-    }
 
     // ---- S5: X = (I + L)^-1 (blocked, fp32); T = X diag(beta) is formed as S6 reads X
     // Diagonal 16x16 blocks, right-looking: column c of block w per lane c.
@@ -1019,83 +1017,129 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         lds_barrier();
     }
 
-    // ---- S6: u = T v (T split) and w^T = (e^G k)^T T^T (single) --------------
+    // ---- S6: T^T kd and Aqk T, T = X diag(beta) --------------------------------
+    // The scan never forms u = T v or w = T (e^G k): with y = v - (e^G k) S,
+    // vnew = u - w S = T y, so the state update takes (T^T kd)^T y and the
+    // output (Aqk T) y. Both are stored as A fragments: a pair of 16x16
+    // result tiles over token rows [32s, 32s+16) and [32s+16, 32s+32) is the
+    // A fragment of token slice s.
+    float *sc = reinterpret_cast<float *>(rec + kOffSc);
     {
-        const int t = 16 * wave + r;
-        const int nS = wave >= 2 ? 2 : 1;  // T is lower triangular
-        bf16x8 Th[2], Tl[2];
+        // T^T fragments of row tile tt = wave (both token slices): lane (r, g)
+        // element e holds T[32s + kperm(g, e)][16 wave + r] (zero where the
+        // token is earlier than the column: X is lower triangular), fp16 hi +
+        // lo with one scale per tile
+        const int tcol = 16 * wave + r;
+        const float bt = sm.beta[tcol];
+        float tx[2][8];
+        float m = 0.f;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            // T = X diag(beta), row t, columns 32s + kperm(gq, e)
-            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.u.mid.X[t][32 * s + 4 * gq]);
-            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.u.mid.X[t][32 * s + 16 + 4 * gq]);
-            const float4 b0 = *reinterpret_cast<const float4 *>(&sm.beta[32 * s + 4 * gq]);
-            const float4 b1 = *reinterpret_cast<const float4 *>(&sm.beta[32 * s + 16 + 4 * gq]);
-            const float x[8] = {x0.x * b0.x, x0.y * b0.y, x0.z * b0.z, x0.w * b0.w,
-                                x1.x * b1.x, x1.y * b1.y, x1.z * b1.z, x1.w * b1.w};
-            split_bf16x8(x, Th[s], Tl[s]);
-        }
-        // v goes over the dead X and LT once every wave holds its T rows
-        lds_barrier();
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            *reinterpret_cast<uint2 *>(&sm.u.late.V[rg + 8 * i][4 * kc]) = vraw[i];
+            for (int e = 0; e < 8; ++e) {
+                tx[s][e] = sm.u.mid.X[32 * s + kperm(gq, e)][tcol] * bt;
+                m = fmaxf(m, fabsf(tx[s][e]));
+            }
         }
-        lds_barrier();
-        // u tiles (mt = wave, vt): A = T rows, B = v (K = token)
-        float um = 0.f;
+        const int sh = f16_shift(wave_max(m));
 #pragma unroll
-        for (int vt = 0; vt < 8; ++vt) {
+        for (int s = 0; s < 2; ++s) {
+            f16x8 hi, lo;
+            split_f16x8(tx[s], sh, hi, lo);
+            sm.u.mid.TT[wave][s][0][lane] = as_u32x4(hi);
+            sm.u.mid.TT[wave][s][1][lane] = as_u32x4(lo);
+        }
+        if (lane == 0) {
+            sm.u.mid.ttinv[wave] = ldexpf(1.f, -sh);
+        }
+    }
+    lds_barrier();
+    float ttinv[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+        ttinv[tt] = sm.u.mid.ttinv[tt];
+    }
+    // T^T B (rows t, B's columns) for the B fragments bh[s] + bl[s] of a
+    // 16-column block (three passes: T hi B hi, T hi B lo, T lo B hi), K =
+    // token slices s >= tt / 2 (T^T is zero below), scaled; the four row
+    // tiles land in x[2][8] in A-fragment order
+    auto ttb = [&](const u32x4 (&bh)[2], const u32x4 (&bl)[2], float scale, float (&x)[2][8], int tmax) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            if (tt > tmax) {
+                break;  // uniform per wave
+            }
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                if (s >= nS) {
-                    break;  // uniform per wave; keeps s (and Th[s]) static
-                }
-                const bf16x8 vb = lds_tr_frag(&sm.u.late.V[0][0], 32 * s, 16 * vt, lane);
-                acc = mfma(Th[s], vb, acc);
-                acc = mfma(Tl[s], vb, acc);
+            for (int s = tt / 2; s < 2; ++s) {
+                const f16x8 th = as_f16x8(sm.u.mid.TT[tt][s][0][lane]);
+                acc = mfma(th, as_f16x8(bh[s]), acc);
+                acc = mfma(th, as_f16x8(bl[s]), acc);
+                acc = mfma(as_f16x8(sm.u.mid.TT[tt][s][1][lane]), as_f16x8(bh[s]), acc);
             }
-            reinterpret_cast<f32x4 *>(rec + kOffU)[(wave * 8 + vt) * 64 + lane] = acc;
-            um = fmaxf(um, fmaxf(fmaxf(fabsf(acc[0]), fabsf(acc[1])), fmaxf(fabsf(acc[2]), fabsf(acc[3]))));
-        }
-        um = wave_max(um);
-        if (lane == 0) {
-            reinterpret_cast<float *>(rec + kOffSc)[kScUmax + wave] = um;
-        }
-        // w^T tiles (mk, nt = wave): A = (e^G k)^T rows k (K = token), B = T^T;
-        // wl1 sums |w| over this lane's columns of row 16 wave + r
-        float wl1 = 0.f;
+            const float f = ttinv[tt] * scale;
 #pragma unroll
-        for (int sp = 0; sp < 4; ++sp) {
-            float x[8];
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int mk = 2 * sp + half;
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    if (s >= nS) {
-                        break;
-                    }
-                    const bf16x8 kb = lds_tr_frag(&sm.u.mid.KE[0][0], 32 * s, 16 * mk, lane);
-                    acc = mfma(kb, Th[s], acc);
-                }
-                // acc[i] = w[16*wave + r][16*mk + 4gq + i]
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    x[4 * half + i] = acc[i];
-                    wl1 += fabsf(acc[i]);
-                }
+            for (int i = 0; i < 4; ++i) {
+                x[tt >> 1][4 * (tt & 1) + i] = acc[i] * f;
             }
-            store_frag_f16(rec, kOffW, wave * 4 + sp, kScW + wave * 4 + sp, lane, x);
         }
-        // the row sums over all 128 columns (four lane groups), then their maximum
-        wl1 += __shfl_xor(wl1, 16);
-        wl1 += __shfl_xor(wl1, 32);
-        wl1 = wave_max(wl1);
-        if (lane == 0) {
-            reinterpret_cast<float *>(rec + kOffSc)[kScWl1 + wave] = wl1;
+    };
+    // (T^T kd) fragments, row tiles mk = 2 wave + tt of kd^T T
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int mk = 2 * wave + tt;
+        float x[2][8];
+        ttb(kdh[tt], kdl[tt], kdinv[tt], x, 3);
+        store_frags_f16<2>(rec, kOffKd, mk * 2, sc + kScKd + mk, lane, x);
+    }
+    if (tracked) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int mk = 2 * wave + tt;
+            float x[2][8];
+            ttb(kth[tt], ktl[tt], ktinv[tt], x, 3);
+            store_frags_f16<2>(tr, kTrOffKd, mk * 2, reinterpret_cast<float *>(tr + kTrOffSc) + mk, lane, x);
+        }
+    }
+    {
+        // (Aqk T) fragments of row tile mt = wave: B = Aqk^T, lane (r, g)
+        // element e = Aqk[16 wave + r][32s + kperm(g, e)] (zero above the
+        // diagonal); tokens after the row's last contribute nothing, so only
+        // the tiles tt <= wave are formed and slice 1 only for wave >= 2
+        const int row = 16 * wave + r;
+        float ax[2][8];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 4 * gq]);
+            const float4 x1 = *reinterpret_cast<const float4 *>(&sm.u.mid.LT[row][32 * s + 16 + 4 * gq]);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                ax[s][e] = 32 * s + kperm(gq, e) <= row ? xv[e] : 0.f;
+            }
+        }
+        u32x4 aqh[2], aql[2];
+        float aqinv;
+        to_frags(ax, aqh, aql, aqinv);
+        float x[2][8];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x[s][e] = 0.f;
+            }
+        }
+        ttb(aqh, aql, aqinv, x, wave);
+        float *asc = sc + kScAq + wave;
+        if (wave < 2) {
+            float x1[1][8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x1[0][e] = x[0][e];
+            }
+            store_frags_f16<1>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x1);
+        } else {
+            store_frags_f16<2>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x);
         }
     }
 }
@@ -1104,75 +1148,74 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 // K2: the serial chunk scan per (sequence, head, CW = 16 NT value columns).
 //
 // Twelve waves in three roles. Every wave meets the same two workgroup
-// barriers per chunk j: B1(j) after S_j is published, B2(j) after vnew_j is.
+// barriers per chunk j: B1(j) after S_j is published, B2(j) after y_j is.
 //   chain waves 0-3   own S rows [32c, 32c+32) x CW columns (fp32, registers)
-//                     and run the recurrence: publish S_j, vnew_j = u - w S_j,
-//                     publish vnew_j, S_{j+1} = e^(G_last) S_j + kd^T vnew_j;
+//                     and run the recurrence: publish S_j, y_j = v - (e^G k)
+//                     S_j, publish y_j, S_{j+1} = e^(G_last) S_j +
+//                     (T^T kd)^T y_j;
 //   output waves 4-7  own token rows [16o, 16o+16): (q e^G) S_j between B2(j)
-//                     and B1(j+1), Aqk vnew_j between B1(j+1) and B2(j+1)
-//                     (Aqk from the stage, vnew_j from its LDS hand-over),
+//                     and B1(j+1), (Aqk T) y_j between B1(j+1) and B2(j+1)
+//                     (Aqk T from the stage, y_j from its LDS hand-over),
 //                     then o_j = the sum and its store after B2(j+1); they
 //                     load their q e^G fragments themselves, a chunk ahead;
-//   loader waves 8-11 copy the chain's operands of chunk j+1 (w, kd^T, Aqk,
-//                     this group's u, e^(G_last), the scales), loaded into
+//   loader waves 8-11 copy the chain's operands of chunk j+1 (e^G k,
+//                     (T^T kd)^T, Aqk T, e^(G_last), the scales) and this
+//                     group's v (with its largest magnitude), loaded into
 //                     their registers after B2(j-2), into the LDS stage of
 //                     j+1's parity between B1(j) and B2(j) (every reader of
 //                     that stage's previous chunk j-1 finished before B1(j)),
 //                     then issue the loads of chunk j+3. The recurrence never
 //                     waits to issue a global load.
-// S_j, vnew_j and the stage are indexed by j's parity; a buffer of parity
+// S_j, y_j and the stage are indexed by j's parity; a buffer of parity
 // j&1 is rewritten only after B1(j+1) or later, when its chunk-j readers are
 // done (the stage after B2(j+1): the output waves read its Aqk until then). One barrier B0 before the first chunk publishes
 // the first stage; one after the last chunk covers the last hand-over.
 //
 // S_j is published as fp16 scaled per 32-row slice (the state itself stays
-// fp32 in registers). vnew is exchanged as fp16 hi + lo scaled by 2^sv, where
-// 2^-sv bounds |vnew| <= max|u| + max_t sum_k |w[t][k]| max|S_j| (both maxima
-// from the record, max|S_j| from the publish) inside [2^13, 2^14): the pair
-// holds vnew to ~2^-22 of that bound and cannot overflow.
+// fp32 in registers). y is exchanged as fp16 hi + lo scaled by 2^sv, where
+// 2^-sv bounds |y| <= max|v| + max_t sum_k |(e^G k)[t][k]| max|S_j| (max|v|
+// from the loaders, the sum from the record, max|S_j| from the publish)
+// inside [2^13, 2^14): the pair holds y to ~2^-22 of that bound and cannot
+// overflow.
 //
-// The chunk operands (~42 KiB of w, kd^T and Aqk plus 16 KiB of q e^G) are
-// the same for every column group of a (sequence, head), so a wider group
-// (NT = 2) reads fewer operand bytes per unit of work; a narrower one
-// (NT = 1) has the shorter serial step. The host picks NT from the number of
-// chains.
+// The chunk operands (~38 KiB of e^G k, (T^T kd)^T and Aqk T plus 16 KiB of
+// q e^G) are the same for every column group of a (sequence, head), so a
+// wider group (NT = 2) reads fewer operand bytes per unit of work; a
+// narrower one (NT = 1) has the shorter serial step. The host picks NT from
+// the number of chains.
 // ---------------------------------------------------------------------------
 
 constexpr int kScanThreads = 768;
-constexpr int kStKd = 16;  // stage fragment indices: w at 0, kd^T, Aqk, then u
+constexpr int kStKd = 16;  // stage fragment indices: e^G k at 0, (T^T kd)^T, Aqk T, then v
 constexpr int kStAq = 32;
-constexpr int kStU = 38;
-static_assert(kOffKd == kStKd * kFrag && kOffAq == kStAq * kFrag && kOffQg == kStU * kFrag &&
+constexpr int kStV = 38;
+static_assert(kOffKd == kStKd * kFrag && kOffAq == kStAq * kFrag && kOffQg == kStV * kFrag &&
                   kOffSc == kOffGl + DK * 4,
               "the stage copies the record's first 38 fragments in order, then gl and the scale block");
 
-// Stage of one chunk for NT column tiles: 38 shared fragments, u (mt, ct) at
-// kStU + mt NT + ct, then e^(G_last) [128] and the scale block [128].
+// Stage of one chunk for NT column tiles: 38 shared fragments from the
+// record, this group's v as a row-major bf16 tile [64][16 NT] at fragment
+// kStV (loaded from the input; its region holds 4 NT fragments), then
+// e^(G_last) [128] and the scale block [128].
 template <int NT>
 struct Stage {
-    static constexpr int kFrags = kStU + 4 * NT + 1;
-    static constexpr int kMisc = (kStU + 4 * NT) * kFrag;
-    static constexpr int kLoadPer = (kFrags + 3) / 4;  // fragments per loader wave
-    // record offset of stage fragment f for column group vt
-    __device__ static int src(int f, int vt) {
-        if (f < kStU) {
-            return f * kFrag;
-        }
-        if (f < kStU + 4 * NT) {
-            const int u = f - kStU;
-            return kOffU + ((u / NT) * 8 + NT * vt + u % NT) * kFrag;
-        }
-        return kOffGl;
-    }
+    static constexpr int kFrags = kStV + 4 * NT + 1;
+    static constexpr int kMisc = (kStV + 4 * NT) * kFrag;
+    static constexpr int kRecFrags = kStV + 1;  // copied from the record: shared fragments, misc
+    static constexpr int kLoadPer = (kRecFrags + 3) / 4;  // record fragments per loader wave
+    // stage and record offsets of record fragment f (the last one is misc)
+    __device__ static int dst(int f) { return f < kStV ? f * kFrag : kMisc; }
+    __device__ static int src(int f) { return f < kStV ? f * kFrag : kOffGl; }
 };
 
 template <int NT>
 struct ScanShared {
     char stg[2][Stage<NT>::kFrags * kFrag];  // chain operands by parity, fragments in lane order
     u32x4 sbuf[2][4][NT][64];                // S_j as fp16 B fragments: [parity][slice][tile][lane]
-    u32x4 vbuf[2][2][2][NT][64];             // vnew_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
+    u32x4 vbuf[2][2][2][NT][64];             // y_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
     float sscale[2][4];                      // 2^-shift of each S_j slice in sbuf
     float smax[2][4];                        // max |S_j| of each slice
+    float vmax[2][4];                        // max |v| of each row tile of the staged v
     uint32_t otile[4][16][8 * NT];           // per output wave: 16 rows x CW bf16 columns
 };
 static_assert(sizeof(ScanShared<2>) <= 160 * 1024, "the scan's LDS budget");
@@ -1332,27 +1375,38 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // write it between B2(j-1) and B1(j)): those of phase B first, then
         // those of phase C behind the first tile's S fragments.
         struct OpsB {
-            f16x8 Wf[4];
-            f32x4 uu[NT];
-            float4 wsc;
-            float umax, wl1;
+            f16x8 Kef[4];
+            f32x4 vv[NT];
+            float4 kesc;
+            float vmax, kel1;
         };
         auto read_b = [&](OpsB &op, int j) {
             const char *st = sm.stg[j & 1];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                op.Wf[s] = stage_frag(st, wr * 4 + s, lane);
+                op.Kef[s] = stage_frag(st, wr * 4 + s, lane);
             }
+            // v C tiles (rows 16 wr + 4gq + i, column 16 ct + r) from the
+            // row-major bf16 tile: transposing reads, then widened
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                op.uu[ct] = reinterpret_cast<const f32x4 *>(st + (kStU + wr * NT + ct) * kFrag)[lane];
+                const int g = lane >> 4;
+                const int m = (lane >> 2) & 3;
+                const int c4 = lane & 3;
+                const uint16_t *vt_tile = reinterpret_cast<const uint16_t *>(st + kStV * kFrag);
+                const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4 *)(vt_tile + (16 * wr + 4 * g + m) * CW + 16 * ct + 4 * c4));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    op.vv[ct][i] = __uint_as_float(static_cast<uint32_t>(static_cast<uint16_t>(x[i])) << 16);
+                }
             }
-            const float4 um = *reinterpret_cast<const float4 *>(sc + kScUmax);
-            op.umax = fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w));
-            op.wsc = *reinterpret_cast<const float4 *>(sc + kScW + 4 * wr);
-            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScWl1);
-            op.wl1 = fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w));
+            const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[j & 1][0]);
+            op.vmax = fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w));
+            op.kesc = *reinterpret_cast<const float4 *>(sc + kScKe + 4 * wr);
+            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScKel1);
+            op.kel1 = fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w));
         };
         auto step = [&](int j) {
             const int p = j & 1;
@@ -1396,15 +1450,15 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             lds_barrier();  // B1(j)
             OpsB ob;
             read_b(ob, j);
-            // B. vnew rows [16wr, 16wr+16) = u - w S_j (one product per slice,
-            // then scaled), published as fp16 hi/lo scaled by 2^sv; tile wr is
-            // half wr%2 of slice wr/2. Phase C's operands of chunk j are read
-            // behind the first tile's S fragments.
+            // B. y rows [16wr, 16wr+16) = v - (e^G k) S_j (one product per
+            // slice, then scaled), published as fp16 hi/lo scaled by 2^sv;
+            // tile wr is half wr%2 of slice wr/2. Phase C's operands of chunk
+            // j are read behind the first tile's S fragments.
             const float4 sx = *reinterpret_cast<const float4 *>(&sm.smax[p][0]);
             const float4 ss = *reinterpret_cast<const float4 *>(&sm.sscale[p][0]);
-            const int sv = f16_shift(ob.umax + ob.wl1 * fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
+            const int sv = f16_shift(ob.vmax + ob.kel1 * fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
             const float inv_v = ldexpf(1.f, -sv);
-            const float fw[4] = {ob.wsc.x * ss.x, ob.wsc.y * ss.y, ob.wsc.z * ss.z, ob.wsc.w * ss.w};
+            const float fw[4] = {ob.kesc.x * ss.x, ob.kesc.y * ss.y, ob.kesc.z * ss.z, ob.kesc.w * ss.w};
             f16x8 Kd[2][2];
             f32x4 gl[2];
             float2 kdsc;
@@ -1413,7 +1467,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 f32x4 acc[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    acc[s] = mfma(ob.Wf[s], as_f16x8(sm.sbuf[p][s][ct][lane]), z4);
+                    acc[s] = mfma(ob.Kef[s], as_f16x8(sm.sbuf[p][s][ct][lane]), z4);
                 }
                 if (ct == 0) {
 #pragma unroll
@@ -1437,7 +1491,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                     for (int s = 0; s < 4; ++s) {
                         x += fw[s] * acc[s][i];
                     }
-                    v[i] = ob.uu[ct][i] - x;
+                    v[i] = ob.vv[ct][i] - x;
                 }
                 uint32_t hp[2], lp[2];
                 split_f16x2(v[0], v[1], sv, hp[0], lp[0]);
@@ -1452,9 +1506,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 vl[hf + 1] = lp[1];
             }
             lds_barrier();  // B2(j)
-            // C. S_{j+1} = e^(G_last) S_j + kd^T vnew_j (fp16 kd against vnew
-            // hi + lo, then both scales), one column tile at a time; the
-            // tracked prefix strictly inside this chunk is taken from S_j
+            // C. S_{j+1} = e^(G_last) S_j + (T^T kd)^T y_j (fp16 (T^T kd)^T
+            // against y hi + lo, then both scales), one column tile at a time;
+            // the tracked prefix strictly inside this chunk is taken from S_j
             // first.
             const int rr = track_len - BT * j;
             const bool track_in = track_slot > 0 && rr > 0 && rr < len;
@@ -1528,21 +1582,22 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     } else if (w < 8) {
         // ------------------------------- output waves ------------------------------
         f32x4 P[NT];  // (q e^G) S of the chunk whose output is pending
-        f32x4 A[NT];  // Aqk vnew of that chunk
+        f32x4 A[NT];  // (Aqk T) y of that chunk
 #pragma unroll
         for (int ct = 0; ct < NT; ++ct) {
             P[ct] = z4;
             A[ct] = z4;
         }
-        // A = Aqk vnew_j for rows [16wr, 16wr+16): Aqk from chunk j's stage
-        // (rewritten only after B2(j+1)), vnew_j hi + lo from vbuf (published
-        // before B2(j), rewritten after B1(j+2)), scaled as the chain scaled it.
-        auto aqk_vnew = [&](int j) {
+        // A = (Aqk T) y_j for rows [16wr, 16wr+16): Aqk T from chunk j's
+        // stage (rewritten only after B2(j+1)), y_j hi + lo from vbuf
+        // (published before B2(j), rewritten after B1(j+2)), scaled as the
+        // chain scaled it.
+        auto aqk_y = [&](int j) {
             const int p = j & 1;
             const char *st = sm.stg[p];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
-            const float4 um = *reinterpret_cast<const float4 *>(sc + kScUmax);
-            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScWl1);
+            const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[p][0]);
+            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScKel1);
             const float4 sx = *reinterpret_cast<const float4 *>(&sm.smax[p][0]);
             const int sv = f16_shift(fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w)) +
                                      fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w)) *
@@ -1625,7 +1680,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             lds_barrier();  // B1(j)
             load_out(other, j + 1);
             if (j > j0) {
-                aqk_vnew(j - 1);
+                aqk_y(j - 1);
             }
             lds_barrier();  // B2(j)
             if (j > j0) {
@@ -1665,40 +1720,76 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         }
         if (j1 > j0) {
             lds_barrier();  // B1(j1)
-            aqk_vnew(j1 - 1);
+            aqk_y(j1 - 1);
             finish(j1 - 1);
         }
     } else {
         // ------------------------------- loader waves ------------------------------
-        // Loader wave wl carries stage fragments wl, wl + 4, ... of a chunk in
-        // registers from their load to their LDS write. Two register sets
-        // (chunks at even / odd distance from j0) keep each chunk's loads in
-        // flight for a chunk and a half: chunk c is loaded after B1(c-2) and
-        // written to the stage of its parity after B2(c-1) (every reader of
-        // that stage's previous chunk c-2 finished before B2(c-1): the chain
-        // reads a stage between B1 and B2 of its chunk).
+        // Loader wave wl carries record fragments wl, wl + 4, ... of a chunk and
+        // this group's v of row tile wl in registers from their load to their
+        // LDS write. Two register sets (chunks at even / odd distance from j0)
+        // keep each chunk's loads in flight for a chunk and a half: chunk c is
+        // loaded after B1(c-2) and written to the stage of its parity after
+        // B2(c-1) (every reader of that stage's previous chunk c-2 finished
+        // before B2(c-1): the chain reads a stage between B1 and B2 of its
+        // chunk, the output waves its Aqk T before B2 of the next).
         constexpr int kPer = St::kLoadPer;
         const int wl = w - 8;
         u32x4 RA[kPer], RB[kPer];
+        uint2 V0[NT], V1[NT], V2[NT], V3[NT];
         // Every loader wave issues the same number of loads (a surplus one
         // repeats the last fragment, which another wave also writes with the
         // same bytes), so the compiler's load counters stay exact and a write
         // waits only for its own set's loads.
         auto frag_of = [&](int k) {
             const int f = wl + 4 * k;
-            return f < St::kFrags ? f : St::kFrags - 1;
+            return f < St::kRecFrags ? f : St::kRecFrags - 1;
         };
+        const uint16_t *vp = static_cast<const uint16_t *>(a.v);
+        // this group's v rows [16 wl, 16 wl + 16) of a chunk, 8 bytes (four
+        // columns) per lane: load k covers rows 16 wl + k (16 / NT) + lane /
+        // (4 NT), columns 4 (lane % (4 NT)); rows past the chunk's end load its
+        // last row and are zeroed
+        auto vrow = [&](int k) { return 16 * wl + k * (16 / NT) + lane / (4 * NT); };
+        auto vcol = [&]() { return 4 * (lane % (4 * NT)); };
         auto fetch = [&](u32x4 (&R)[kPer], int j) {
             const char *rec = rec_of(j < j1 ? j : j1 - 1);
 #pragma unroll
             for (int k = 0; k < kPer; ++k) {
-                R[k] = reinterpret_cast<const u32x4 *>(rec + St::src(frag_of(k), vt))[lane];
+                R[k] = reinterpret_cast<const u32x4 *>(rec + St::src(frag_of(k)))[lane];
             }
         };
-        auto put = [&](const u32x4 (&R)[kPer], int par) {
+        auto fetch_v = [&](uint2 (&V)[NT], int j) {
+            const int jc = j < j1 ? j : j1 - 1;
+            const int t0 = bos + BT * jc;
+            const int len = eos - t0 < BT ? eos - t0 : BT;
+#pragma unroll
+            for (int k = 0; k < NT; ++k) {
+                const int row = vrow(k);
+                const int tc = row < len ? row : len - 1;
+                V[k] = *reinterpret_cast<const uint2 *>(vp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + col0 +
+                                                        vcol());
+                const uint32_t keep = keep_mask(row < len);
+                V[k].x &= keep;
+                V[k].y &= keep;
+            }
+        };
+        auto put = [&](const u32x4 (&R)[kPer], const uint2 (&V)[NT], int par) {
 #pragma unroll
             for (int k = 0; k < kPer; ++k) {
-                reinterpret_cast<u32x4 *>(sm.stg[par] + frag_of(k) * kFrag)[lane] = R[k];
+                reinterpret_cast<u32x4 *>(sm.stg[par] + St::dst(frag_of(k)))[lane] = R[k];
+            }
+            uint16_t *vt_tile = reinterpret_cast<uint16_t *>(sm.stg[par] + kStV * kFrag);
+            uint32_t m = 0;  // largest |v| as bf16 bits (order-preserving for magnitudes)
+#pragma unroll
+            for (int k = 0; k < NT; ++k) {
+                *reinterpret_cast<uint2 *>(vt_tile + vrow(k) * CW + vcol()) = V[k];
+                m = max(m, max(max(V[k].x & 0x7fffu, (V[k].x >> 16) & 0x7fffu),
+                               max(V[k].y & 0x7fffu, (V[k].y >> 16) & 0x7fffu)));
+            }
+            const float mf = wave_max(__uint_as_float(m << 16));
+            if (lane == 0) {
+                sm.vmax[par][wl] = mf;
             }
         };
         // L2 warm-up: at chunk j each workgroup reads one dword of each line of
@@ -1727,30 +1818,47 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 dst[k] = *reinterpret_cast<const uint32_t *>(rec + l * 128);
             }
         };
-        // Chunk j+2 is loaded after B1(j) into the set chunk j left (written
-        // after B2(j-1)), chunk j+1 goes into the stage of its parity after
-        // B2(j). Indices past the end are clamped to the last chunk: the extra
-        // copies land in a stage no one reads again, and every wait count on
-        // the loop's path stays exact.
-        auto iter = [&](u32x4 (&Rload)[kPer], const u32x4 (&Rput)[kPer], uint32_t (&dst)[kTouch], int j) {
+        // Chunk j+2's record fragments are loaded after B1(j) into the set
+        // chunk j left (written after B2(j-1)), and chunk j+3's v into the
+        // one of four v sets chunk j-1 left (v, read straight from the input,
+        // gets the longer head start); chunk j+1 goes into the stage of its
+        // parity after B2(j). Indices past the end are clamped to the last
+        // chunk: the extra copies land in a stage no one reads again, and
+        // every wait count on the loop's path stays exact.
+        auto iter = [&](u32x4 (&Rload)[kPer], const u32x4 (&Rput)[kPer], uint2 (&Vload)[NT],
+                        const uint2 (&Vput)[NT], uint32_t (&dst)[kTouch], int j) {
             lds_barrier();  // B1(j)
             fetch(Rload, j + 2);
+            fetch_v(Vload, j + 3);
             touch(dst, j + kWarmAhead);
             lds_barrier();  // B2(j)
-            put(Rput, (j + 1) & 1);
+            put(Rput, Vput, (j + 1) & 1);
         };
         if (j1 > j0) {
             fetch(RA, j0);
-            put(RA, j0 & 1);
+            fetch_v(V0, j0);
+            fetch_v(V1, j0 + 1);
+            fetch_v(V2, j0 + 2);
+            put(RA, V0, j0 & 1);
             fetch(RB, j0 + 1);
         }
         lds_barrier();  // B0
-        for (int j = j0; j < j1; j += 2) {
-            iter(RA, RB, wa, j);  // loads chunk j+2 (even distance), writes j+1
+        // chunk c's record fragments are in RA when c - j0 is even, else RB;
+        // its v in V0..V3 by (c - j0) % 4
+        for (int j = j0; j < j1; j += 4) {
+            iter(RA, RB, V3, V1, wa, j);
             if (j + 1 >= j1) {
                 break;
             }
-            iter(RB, RA, wb, j + 1);  // loads j+3, writes j+2
+            iter(RB, RA, V0, V2, wb, j + 1);
+            if (j + 2 >= j1) {
+                break;
+            }
+            iter(RA, RB, V1, V3, wa, j + 2);
+            if (j + 3 >= j1) {
+                break;
+            }
+            iter(RB, RA, V2, V0, wb, j + 3);
         }
         if (j1 > j0) {
             lds_barrier();  // B1(j1)

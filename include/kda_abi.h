@@ -219,10 +219,11 @@ int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,
  * forbid hipMalloc). The workspace is a static device array of
  * KDA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; its address
  * on a device is resolved on the first call on that device. Several sequences
- * whose records do not fit it (at K = V = 128 roughly 750 (chunk, head)
- * pairs, e.g. 1024 tokens on 32 heads) return KDA_ERR_TOO_LARGE; a single
- * sequence of any length runs in windows of the chunks it holds (the small-
- * workspace form of kda_chunk_launch: about 750 / H chunks, 23 on 32 heads).
+ * whose records do not fit it (at K = V = 128 roughly 1190 (chunk, head)
+ * pairs, e.g. 2 x 2048 tokens on 32 heads) return KDA_ERR_TOO_LARGE; a
+ * single sequence of any length runs in windows of the chunks it holds (the
+ * small-workspace form of kda_chunk_launch: about 1190 / H chunks, 37 on 32
+ * heads).
  * Results are those of kda_chunk_launch on the same arguments; no second
  * stream is used. Every call on one GPU shares that GPU's array (its
  * contents need no initialization, the last call's are left behind): calls

@@ -146,7 +146,7 @@ def test_chunk_launch_alignment_checks_need_no_device(lib):
 
 def test_chunk_workspace_size_formula(lib):
     """kda_chunk_workspace_bytes is a host-only function of (T, N, H, D): the
-    chunk-start table, 87 KiB records, one 16.75 KiB tracking record per
+    chunk-start table, 55 KiB records, one 16.75 KiB tracking record per
     (sequence, head) and, for a single sequence, one 64 KiB state per head
     carried between scan segments, each 256-byte aligned (the sizes the
     integration notes quote for sizing a reusable workspace). The records: one
@@ -156,8 +156,8 @@ def test_chunk_workspace_size_formula(lib):
     each) and needs a ring of two of the longest per head."""
     lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
     lib.kda_chunk_workspace_bytes.argtypes = [ctypes.c_int32] * 4
-    rec, track = 89088, 17152
-    assert rec == 87 * 1024 and track == 16.75 * 1024
+    rec, track = 56320, 17152
+    assert rec == 55 * 1024 and track == 16.75 * 1024
     for T, N, H in [(8192, 1, 32), (33814, 16, 32), (65536, 1, 16), (65536, 1, 17), (16383, 1, 4),
                     (16384, 1, 4), (100000, 1, 8), (1, 1, 1), (0, 3, 2)]:
         header = ((N + 1) * 4 + 255) // 256 * 256

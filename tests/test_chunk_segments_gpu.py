@@ -21,7 +21,12 @@ from tests.test_zz_no_alloc import _lib, _prepare
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-REC = 89088  # bytes per (chunk, head) record
+
+
+def _rec_bytes(lib):
+    """Bytes per (chunk, head) record: what one more chunk of a two-sequence
+    batch adds to kda_chunk_workspace_bytes on one head."""
+    return lib.kda_chunk_workspace_bytes(128, 2, 1, 128) - lib.kda_chunk_workspace_bytes(64, 2, 1, 128)
 
 
 def _launch(lib, case, nbytes, track=None):
@@ -58,6 +63,7 @@ def test_small_workspace_runs_segments(label, lens, bounds, window, track):
     if bounds is not None:
         case = dataclasses.replace(case, cu_seqlens=torch.tensor(bounds, dtype=torch.int32))
     T, H, D = case.q.shape[1:]
+    REC = _rec_bytes(lib)
     full = lib.kda_chunk_workspace_bytes(T, 1, H, D)
     base = full - REC * ((T + 63) // 64 + 1) * H
     small = base + REC * window * H
@@ -79,6 +85,7 @@ def test_pipelined_segments_match_sequential_segments():
     lib = _lib()
     case = C.prepared_case(4, (16384,), slots=3, indices=[1], seed=95)
     T, H, D = case.q.shape[1:]
+    REC = _rec_bytes(lib)
     ring = lib.kda_chunk_workspace_bytes(T, 1, H, D)
     base = ring - REC * 2 * 136 * H  # two segments, 120 and 136 chunks
     rc_a, out_a, pool_a = _launch(lib, case, ring, (2, 9000))

@@ -11,12 +11,13 @@ large for it is refused before anything is written.
 """
 
 import ctypes
+import re
 
 import pytest
 import torch
 
 from tests import kda_cases as C
-from tests.test_abi_exports import _ChunkArgs
+from tests.test_abi_exports import HEADER, _ChunkArgs
 
 pytestmark = pytest.mark.gpu
 
@@ -114,7 +115,11 @@ def test_noalloc_refuses_oversized_call_untouched():
     can run in segments) returns KDA_ERR_TOO_LARGE and writes nothing."""
     lib = _lib()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    case = C.prepared_case(32, (1024, 1024), slots=3, indices=[1, 2], seed=73)
+    case = C.prepared_case(32, (2048, 2048), slots=3, indices=[1, 2], seed=73)
+    T, H, D = case.q.shape[1:]
+    limit = int(re.search(r"KDA_NOALLOC_SCRATCH_BYTES\s+\((\d+)u \* 1024u \* 1024u\)",
+                          open(HEADER).read()).group(1)) << 20
+    assert lib.kda_chunk_workspace_bytes(T, 2, H, D) > limit
     a, out, pool, keep = _prepare(case)
     before = pool.clone()
     assert lib.kda_chunk_launch_noalloc(ctypes.byref(a), stream) == 5
