@@ -319,22 +319,16 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
 // ---------------------------------------------------------------------------
 // K1: per (chunk, head) intra-chunk work.
 //
-// 53 KiB of LDS (two workgroups per CU, which its registers also allow; at
-// three, forced, it ran no faster). The chunk's k, g, beta and each wave's q
-// rows are loaded up front, v after the cumsum and k tiles die. k stays as
-// its bf16 input plus a per-row inverse norm; the decay is accumulated in
-// log2 units, so each exponential is one v_exp_f32. v and e^G k stay
-// row-major and are read as MFMA operands with gfx950's transposing LDS read
-// ds_read_b64_tr_b16: within each group of 16 lanes, lane 16G + i receives as
-// element m the (i % 4)-th 16-bit value of the 8-byte word addressed by lane
-// 16G + 4m + i / 4. X, LT and e^G k lie over the cumsum and k tiles once
-// those are dead, and v over X and LT in the last stage.
+// 67 KiB of LDS (two workgroups per CU, which its registers allow; at three,
+// forced, it ran no faster). The chunk's k, g, beta and each wave's q rows
+// are loaded up front (v is not read here). k is normalized once and kept
+// in fp32, so every operand built from it reads ready values; the decay is
+// accumulated in log2 units, so each exponential is one v_exp_f32. X, LT and
+// the T^T fragments lie over the cumsum and k tiles once those are dead.
 // ---------------------------------------------------------------------------
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kPadF = 132;  // fp32 row stride of [64][128] tiles (16-lane float4 reads)
-constexpr int kPadK = 136;  // bf16 row stride of the k tile (32-lane 8-byte reads)
-constexpr int kPadT = 144;  // bf16 row stride of tiles read transposed
 constexpr int kPadX = 68;   // fp32 row stride of [64][64] tiles (16-B rows)
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -353,30 +347,17 @@ __device__ __forceinline__ uint32_t keep_mask(bool keep) {
     return m;
 }
 
+// gfx950's transposing LDS read ds_read_b64_tr_b16: within each group of 16
+// lanes, lane 16G + i receives as element m the (i % 4)-th 16-bit value of
+// the 8-byte word addressed by lane 16G + 4m + i / 4.
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// MFMA operand from a row-major bf16 LDS tile (row stride PAD elements, a
-// multiple of 4) whose rows are the K index: lane (r, g) receives
-// tile[row0 + kperm(g, e)][col0 + r], e = 0..7 (two transposing reads, rows
-// row0 + 4g + m and row0 + 16 + 4g + m).
-template <int PAD = kPadT>
-__device__ __forceinline__ bf16x8 lds_tr_frag(const uint16_t *tile, int row0, int col0, int lane) {
-    static_assert(PAD % 4 == 0, "8-byte aligned rows");
-    const int g = lane >> 4;
-    const int m = (lane >> 2) & 3;
-    const int c4 = lane & 3;
-    const uint16_t *p0 = tile + (row0 + 4 * g + m) * PAD + col0 + 4 * c4;
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p0 + 16 * PAD));
-    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
 
 struct PrepShared {
     union {
         struct {
             float G[BT][kPadF];     // cumsum of the log2 decay (S1-S4)
-            uint16_t K[BT][kPadK];  // k, bf16 input bits (S1-S4)
+            float K[BT][kPadF];     // k normalized (or as is), fp32 (S1-S4)
             float qss[2][BT];       // sum of q^2 over each channel half, per row (S1-S3)
         } early;
         struct {
@@ -389,10 +370,9 @@ struct PrepShared {
         } mid;
     } u;
     float beta[BT];
-    float rnk[BT];        // k row scale (1 / norm, or 1)
     float carry[DK];
 };
-static_assert(sizeof(PrepShared) <= 54 * 1024, "the prepare kernel's LDS budget");
+static_assert(sizeof(PrepShared) <= 80 * 1024, "two prepare workgroups per CU");
 
 // Chunks [c_lo, c_hi) of the launch (global chunk indices: one sequence's
 // own chunks, or all sequences' through the chunk index); chunk c's record
@@ -558,19 +538,12 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int t = rg + 8 * i;
-            if (norm) {
-                const float4 k4 = make_float4(__uint_as_float(kraw[i].x << 16),
-                                              __uint_as_float(kraw[i].x & 0xffff0000u),
-                                              __uint_as_float(kraw[i].y << 16),
-                                              __uint_as_float(kraw[i].y & 0xffff0000u));
-                const float ks = group_sum32(dot4(k4, k4));
-                if (kc == 0) {
-                    sm.rnk[t] = 1.0f / sqrtf(ks + 1e-6f);
-                }
-            } else if (kc == 0) {
-                sm.rnk[t] = 1.0f;
-            }
-            *reinterpret_cast<uint2 *>(&sm.u.early.K[t][4 * kc]) = kraw[i];
+            const float4 k4 = make_float4(__uint_as_float(kraw[i].x << 16), __uint_as_float(kraw[i].x & 0xffff0000u),
+                                          __uint_as_float(kraw[i].y << 16), __uint_as_float(kraw[i].y & 0xffff0000u));
+            // the row's 1 / norm (every lane of the 32-lane row group holds it)
+            const float rn = norm ? 1.0f / sqrtf(group_sum32(dot4(k4, k4)) + 1e-6f) : 1.0f;
+            *reinterpret_cast<float4 *>(&sm.u.early.K[t][4 * kc]) =
+                make_float4(k4.x * rn, k4.y * rn, k4.z * rn, k4.w * rn);
             *reinterpret_cast<float4 *>(&sm.u.early.G[t][4 * kc]) =
                 make_float4(g4[i].x * kLog2e, g4[i].y * kLog2e, g4[i].z * kLog2e, g4[i].w * kLog2e);
         }
@@ -629,19 +602,19 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     }
     lds_barrier();
 
-    // 8 channels {32s + kperm(gq, e)} of one row: two 8-byte k reads, two
-    // 16-byte G reads.
+    // 8 channels {32s + kperm(gq, e)} of one row: two 16-byte reads each
+    // from the (normalized) k and the cumsum tiles.
     auto load_k8 = [&](int row, int s, float x[8]) {
-        const uint2 k0 = *reinterpret_cast<const uint2 *>(&sm.u.early.K[row][32 * s + 4 * gq]);
-        const uint2 k1 = *reinterpret_cast<const uint2 *>(&sm.u.early.K[row][32 * s + 16 + 4 * gq]);
-        x[0] = __uint_as_float(k0.x << 16);
-        x[1] = __uint_as_float(k0.x & 0xffff0000u);
-        x[2] = __uint_as_float(k0.y << 16);
-        x[3] = __uint_as_float(k0.y & 0xffff0000u);
-        x[4] = __uint_as_float(k1.x << 16);
-        x[5] = __uint_as_float(k1.x & 0xffff0000u);
-        x[6] = __uint_as_float(k1.y << 16);
-        x[7] = __uint_as_float(k1.y & 0xffff0000u);
+        const float4 k0 = *reinterpret_cast<const float4 *>(&sm.u.early.K[row][32 * s + 4 * gq]);
+        const float4 k1 = *reinterpret_cast<const float4 *>(&sm.u.early.K[row][32 * s + 16 + 4 * gq]);
+        x[0] = k0.x;
+        x[1] = k0.y;
+        x[2] = k0.z;
+        x[3] = k0.w;
+        x[4] = k1.x;
+        x[5] = k1.y;
+        x[6] = k1.z;
+        x[7] = k1.w;
     };
     auto load_g8 = [&](int row, int s, float x[8]) {
         const float4 g0 = *reinterpret_cast<const float4 *>(&sm.u.early.G[row][32 * s + 4 * gq]);
@@ -686,7 +659,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         for (int sl = 0; sl < 2; ++sl) {
             load_g8(16 * I + kAnchorRow, 2 * sh + sl, anc[sl]);
         }
-        const float rki = sm.rnk[ri];
         bf16x8 Rh[2], Qh[2], Ql[2];
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
@@ -698,7 +670,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             for (int e = 0; e < 8; ++e) {
                 const float ex = ex2(fminf(gg[e] - anc[sl][e], kMaxExp2));
                 const float qn = qv[sl][e] * qscale;
-                rv[e] = kk[e] * rki * ex;
+                rv[e] = kk[e] * ex;
                 qa[e] = qn * ex;
                 qg[e] = qn * ex2(gg[e]);
             }
@@ -713,7 +685,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 break;  // uniform per wave
             }
             const int rj = 16 * J + r;
-            const float rkj = sm.rnk[rj];
             f32x4 akk = {0.f, 0.f, 0.f, 0.f};
             f32x4 aqt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -724,7 +695,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 load_g8(rj, s, gg);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    cv[e] = kk[e] * rkj * ex2(fminf(anc[sl][e] - gg[e], kMaxExp2));
+                    cv[e] = kk[e] * ex2(fminf(anc[sl][e] - gg[e], kMaxExp2));
                 }
                 bf16x8 Ch, Cl;
                 split_bf16x8(cv, Ch, Cl);
@@ -741,16 +712,12 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
 
     // ---- S4: kd fragments (kept for S6), e^(G_last), tracking operands, e^G k
     // fragments of the record --------------------------------------------------
-    // k[t][16mk + r] rnk[t] for the rows t = 32s + kperm(gq, e) of a kd^T
-    // fragment: k by transposing reads, the row scales as two float4 reads.
+    // k[t][16mk + r] for the rows t = 32s + kperm(gq, e) of a kd^T fragment:
+    // eight column reads (rows 4 apart land 16 banks apart, so none conflict)
     auto kd_rows = [&](int s, int mk, float (&kr)[8]) {
-        const bf16x8 kb = lds_tr_frag<kPadK>(&sm.u.early.K[0][0], 32 * s, 16 * mk, lane);
-        const float4 rn0 = *reinterpret_cast<const float4 *>(&sm.rnk[32 * s + 4 * gq]);
-        const float4 rn1 = *reinterpret_cast<const float4 *>(&sm.rnk[32 * s + 16 + 4 * gq]);
-        const float rn[8] = {rn0.x, rn0.y, rn0.z, rn0.w, rn1.x, rn1.y, rn1.z, rn1.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            kr[e] = static_cast<float>(kb[e]) * rn[e];
+            kr[e] = sm.u.early.K[32 * s + kperm(gq, e)][16 * mk + r];
         }
     };
     // kd[t][16mk + r] = k_t e^(G_last - G_t) for the rows t = 32s + kperm(gq, e)
@@ -841,7 +808,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
     // rows of sum_k |e^G k| bounds that product with max |S|.
     {
         const int row = 16 * wave + r;
-        const float rk = sm.rnk[row];
         float x[4][8];
         float l1 = 0.f;
 #pragma unroll
@@ -851,7 +817,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             load_g8(row, s, gg);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                x[s][e] = kk[e] * rk * ex2(gg[e]);
+                x[s][e] = kk[e] * ex2(gg[e]);
                 l1 += fabsf(x[s][e]);
             }
         }
