@@ -97,7 +97,7 @@ constexpr int kRecBytes = kOffSc + 512;           // 56320
 // Scale block: 2^-shift of each fp16 fragment group, and the bound the scan
 // derives y's scale from (|y| <= max|v| + kel1 max|S|).
 constexpr int kScKe = 0;     // [16] e^G k fragment (mt, s): mt * 4 + s (equal over s)
-constexpr int kScQg = 16;    // [16] q e^G fragment (mt, s)
+constexpr int kScQg = 16;    // [16] q e^G fragment (mt, s) (equal within s = 0, 1 and s = 2, 3)
 constexpr int kScKd = 32;    // [8]  (T^T kd)^T row tile mk (both token slices)
 constexpr int kScAq = 40;    // [4]  Aqk T row tile mt (both token slices)
 constexpr int kScKel1 = 48;  // [4]  max over the rows t of tile mt of sum_k |(e^G k)[t][k]|
@@ -195,14 +195,20 @@ __device__ __forceinline__ f16x8 to_f16x8(const float x[8], int sh) {
     }
     return h;
 }
-// x * 2^sh = hi + lo to about 2^-22 relative (fp16, round to nearest even)
+// x * 2^sh = hi + lo to about 2^-22 relative (fp16, round to nearest even),
+// converted in pairs (one packed conversion per two values)
 __device__ __forceinline__ void split_f16x8(const float x[8], int sh, f16x8 &hi, f16x8 &lo) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float xs = ldexpf(x[e], sh);
-        const _Float16 h = static_cast<_Float16>(xs);
-        hi[e] = h;
-        lo[e] = static_cast<_Float16>(xs - static_cast<float>(h));
+    for (int p = 0; p < 4; ++p) {
+        const f32x2_t xs = {ldexpf(x[2 * p], sh), ldexpf(x[2 * p + 1], sh)};
+        const f16x2_t h = __builtin_convertvector(xs, f16x2_t);
+        const f16x2_t l = __builtin_convertvector(xs - __builtin_convertvector(h, f32x2_t), f16x2_t);
+        hi[2 * p] = h[0];
+        hi[2 * p + 1] = h[1];
+        lo[2 * p] = l[0];
+        lo[2 * p + 1] = l[1];
     }
 }
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
@@ -247,22 +253,7 @@ __device__ __forceinline__ void store_frags_f16(char *base, int off, int idx, fl
         sc[lane] = ldexpf(1.f, -sh);
     }
 }
-__device__ __forceinline__ void store_frag_f16(char *rec, int off, int idx, int sc_idx, int lane,
-                                               const float x[8]) {
-    float y[1][8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        y[0][e] = x[e];
-    }
-    store_frags_f16<1>(rec, off, idx, reinterpret_cast<float *>(rec + kOffSc) + sc_idx, lane, y);
-}
 
-__device__ __forceinline__ void store_frag(char *base, int off, int idx, int lane, bf16x8 v) {
-    reinterpret_cast<u32x4 *>(base + off)[idx * 64 + lane] = as_u32x4(v);
-}
-__device__ __forceinline__ bf16x8 load_frag(const char *base, int off, int idx, int lane) {
-    return as_bf16x8(reinterpret_cast<const u32x4 *>(base + off)[idx * 64 + lane]);
-}
 
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
 // accesses, not for its outstanding global loads (a full __syncthreads() also
@@ -660,10 +651,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             load_g8(16 * I + kAnchorRow, 2 * sh + sl, anc[sl]);
         }
         bf16x8 Rh[2], Qh[2], Ql[2];
+        float qg[2][8];  // q e^G of this half's two slices: one record scale
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
             const int s = 2 * sh + sl;
-            float kk[8], gg[8], rv[8], qa[8], qg[8];
+            float kk[8], gg[8], rv[8], qa[8];
             load_k8(ri, s, kk);
             load_g8(ri, s, gg);
 #pragma unroll
@@ -672,12 +664,13 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
                 const float qn = qv[sl][e] * qscale;
                 rv[e] = kk[e] * ex;
                 qa[e] = qn * ex;
-                qg[e] = qn * ex2(gg[e]);
+                qg[sl][e] = qn * ex2(gg[e]);
             }
             Rh[sl] = to_bf16x8(rv);
             split_bf16x8(qa, Qh[sl], Ql[sl]);
-            store_frag_f16(rec, kOffQg, I * 4 + s, kScQg + I * 4 + s, lane, qg);
         }
+        store_frags_f16<2>(rec, kOffQg, I * 4 + 2 * sh, reinterpret_cast<float *>(rec + kOffSc) + kScQg + I * 4 + 2 * sh,
+                           lane, qg, 2);
         // pairs (I, J), J <= I, over this half's channels
 #pragma unroll
         for (int J = 0; J < (ii == 0 ? 4 : 2); ++J) {
