@@ -367,10 +367,12 @@ static_assert(sizeof(PrepShared) <= 80 * 1024, "two prepare workgroups per CU");
 
 // Chunks [c_lo, c_hi) of the launch (global chunk indices: one sequence's
 // own chunks, or all sequences' through the chunk index); chunk c's record
-// goes to ring slot c % ring.
+// goes to ring slot c % ring. Two workgroups per CU is what the LDS allows,
+// so the register budget is that of two waves per SIMD (256 per lane): the
+// compiler then keeps S3's MFMA results in VGPRs instead of AGPRs.
 template <int GATE>
-__global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkArgs a, char *ws,
-                                                                 int ring, int c_lo, int c_hi) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_prepare_kernel(
+    const KdaChunkArgs a, char *ws, int ring, int c_lo, int c_hi) {
     __shared__ PrepShared sm;
     // Workgroups run chunk-descending, heads fastest: the scan starts with the
     // first chunk of every sequence and head, so those records are written
@@ -516,10 +518,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             if constexpr (GATE == KDA_GATE_RAW) {
                 const float4 av = g4[i];
                 const float lb = a.lower_bound;
-                g4[i].x = lb / (1.0f + __expf(-(expA * (av.x + dtb.x))));
-                g4[i].y = lb / (1.0f + __expf(-(expA * (av.y + dtb.y))));
-                g4[i].z = lb / (1.0f + __expf(-(expA * (av.z + dtb.z))));
-                g4[i].w = lb / (1.0f + __expf(-(expA * (av.w + dtb.w))));
+                // lb * sigmoid(x), the reciprocal as v_rcp_f32 (within 1 ulp)
+                g4[i].x = lb * __builtin_amdgcn_rcpf(1.0f + __expf(-(expA * (av.x + dtb.x))));
+                g4[i].y = lb * __builtin_amdgcn_rcpf(1.0f + __expf(-(expA * (av.y + dtb.y))));
+                g4[i].z = lb * __builtin_amdgcn_rcpf(1.0f + __expf(-(expA * (av.z + dtb.z))));
+                g4[i].w = lb * __builtin_amdgcn_rcpf(1.0f + __expf(-(expA * (av.w + dtb.w))));
             }
             g4[i].x = __uint_as_float(__float_as_uint(g4[i].x) & keep);
             g4[i].y = __uint_as_float(__float_as_uint(g4[i].y) & keep);
@@ -531,8 +534,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
             const int t = rg + 8 * i;
             const float4 k4 = make_float4(__uint_as_float(kraw[i].x << 16), __uint_as_float(kraw[i].x & 0xffff0000u),
                                           __uint_as_float(kraw[i].y << 16), __uint_as_float(kraw[i].y & 0xffff0000u));
-            // the row's 1 / norm (every lane of the 32-lane row group holds it)
-            const float rn = norm ? 1.0f / sqrtf(group_sum32(dot4(k4, k4)) + 1e-6f) : 1.0f;
+            // the row's 1 / norm (every lane of the 32-lane row group holds it;
+            // v_rsq_f32, within 1 ulp, where 1 / sqrtf takes ~30 instructions)
+            const float rn = norm ? __builtin_amdgcn_rsqf(group_sum32(dot4(k4, k4)) + 1e-6f) : 1.0f;
             *reinterpret_cast<float4 *>(&sm.u.early.K[t][4 * kc]) =
                 make_float4(k4.x * rn, k4.y * rn, k4.z * rn, k4.w * rn);
             *reinterpret_cast<float4 *>(&sm.u.early.G[t][4 * kc]) =
@@ -541,7 +545,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         if (tid < BT) {
             float b = braw;
             if constexpr (GATE == KDA_GATE_RAW) {
-                b = 1.0f / (1.0f + __expf(-b));
+                b = __builtin_amdgcn_rcpf(1.0f + __expf(-b));
             }
             sm.beta[tid] = tid < len ? b : 0.f;
         }
@@ -636,7 +640,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prepare_kernel(const KdaChunkA
         q8(ii, 1, qv[1]);
         float qscale = a.scale;
         if (norm) {
-            qscale = a.scale / sqrtf(sm.u.early.qss[0][ri] + sm.u.early.qss[1][ri] + 1e-6f);
+            qscale = a.scale * __builtin_amdgcn_rsqf(sm.u.early.qss[0][ri] + sm.u.early.qss[1][ri] + 1e-6f);
         }
         // The block's anchor row G[16I + 7][.]: a row factor e^(G_i - anchor)
         // of the block spans at most 7 tokens of decay above 1, a column
