@@ -433,38 +433,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     //        wave 2: (2,0) (1,0)   wave 3: (2,1) (1,1)
     const int sh = wave & 1;
     const int IA = wave < 2 ? 3 : 2;
-    // q rows of both blocks in this wave's channel half, loaded now so the
-    // loads overlap S1/S2: lane (r, gq) holds q[16I + r][32s + kperm(gq, e)]
-    // as 2 x (4 bf16) for slices s = 2 sh + q2.
+    // q rows of both blocks in this wave's channel half (loaded in S1, after
+    // k, g and beta, which S1 needs first): lane (r, gq) holds
+    // q[16I + r][32s + kperm(gq, e)] as 2 x (4 bf16) for slices s = 2 sh + q2
     uint2 qraw[2][2][2];
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-        const int t = 16 * (ii == 0 ? IA : 3 - IA) + r;
-#pragma unroll
-        for (int q2 = 0; q2 < 2; ++q2) {
-            const int s = 2 * sh + q2;
-            const int tc = t < len ? t : len - 1;
-            const uint16_t *row = qp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + 32 * s;
-            qraw[ii][q2][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
-            qraw[ii][q2][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
-        }
-    }
-    // padding rows of q are zeroed (loaded from a row clamped into the chunk)
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-        const uint32_t keep = keep_mask(16 * (ii == 0 ? IA : 3 - IA) + r < len);
-#pragma unroll
-        for (int q2 = 0; q2 < 2; ++q2) {
-            qraw[ii][q2][0].x &= keep;
-            qraw[ii][q2][0].y &= keep;
-            qraw[ii][q2][1].x &= keep;
-            qraw[ii][q2][1].y &= keep;
-        }
-    }
-    // widened q: 8 channels {32s + kperm(gq, e)} of slice s = 2 sh + q2
+    // widened q: 8 channels {32s + kperm(gq, e)} of slice s = 2 sh + q2, the
+    // padding rows zeroed (loaded from a row clamped into the chunk)
     auto q8 = [&](int ii, int q2, float x[8]) {
-        const uint2 q0 = qraw[ii][q2][0];
-        const uint2 q1 = qraw[ii][q2][1];
+        const uint32_t keep = keep_mask(16 * (ii == 0 ? IA : 3 - IA) + r < len);
+        const uint2 q0 = make_uint2(qraw[ii][q2][0].x & keep, qraw[ii][q2][0].y & keep);
+        const uint2 q1 = make_uint2(qraw[ii][q2][1].x & keep, qraw[ii][q2][1].y & keep);
         x[0] = __uint_as_float(q0.x << 16);
         x[1] = __uint_as_float(q0.x & 0xffff0000u);
         x[2] = __uint_as_float(q0.y << 16);
@@ -475,7 +453,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         x[7] = __uint_as_float(q1.y & 0xffff0000u);
     };
 
-    // ---- S1: k rows, log2 decay, beta, v (zero-padded) ---------------------
+    // ---- S1: k rows, log2 decay, beta (zero-padded); the q rows' loads ------
     const int kc = tid & 31;
     const int rg = tid >> 5;
     {
@@ -508,6 +486,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 g4[i] = load4(static_cast<const uint16_t *>(a.gate) + base);
             } else {
                 g4[i] = load4(static_cast<const float *>(a.gate) + base);
+            }
+        }
+        // the q rows, behind them
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const int t = 16 * (ii == 0 ? IA : 3 - IA) + r;
+#pragma unroll
+            for (int q2 = 0; q2 < 2; ++q2) {
+                const int s = 2 * sh + q2;
+                const int tc = t < len ? t : len - 1;
+                const uint16_t *row = qp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + 32 * s;
+                qraw[ii][q2][0] = *reinterpret_cast<const uint2 *>(row + 4 * gq);
+                qraw[ii][q2][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
             }
         }
 #pragma unroll
