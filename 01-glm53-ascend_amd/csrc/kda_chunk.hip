@@ -361,7 +361,7 @@ struct PrepShared {
         } mid;
     } u;
     float beta[BT];
-    float carry[DK];
+    float gsum[4][DK];  // each wave's two row groups' decay sums (the cumsum's carries)
 };
 static_assert(sizeof(PrepShared) <= 80 * 1024, "two prepare workgroups per CU");
 
@@ -456,6 +456,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // ---- S1: k rows, log2 decay, beta (zero-padded); the q rows' loads ------
     const int kc = tid & 31;
     const int rg = tid >> 5;
+    float4 gcum[8];  // the in-chunk prefix of this lane's rows, then the cumsum
+    float4 gprev;    // the partner row group's sum (odd rg) or zero
     {
         const uint16_t *kp = static_cast<const uint16_t *>(a.k);
         float expA = 0.f;
@@ -474,11 +476,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         } else {
             braw = static_cast<const float *>(a.beta)[static_cast<int64_t>(t0 + tb) * H + h];
         }
+        // lane (rg, kc) carries rows 8 rg .. 8 rg + 7, channels 4 kc .. 4 kc + 3
         uint2 kraw[8];
         float4 g4[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int t = rg + 8 * i;
+            const int t = 8 * rg + i;
             const int tc = t < len ? t : len - 1;
             const int64_t base = (static_cast<int64_t>(t0 + tc) * H + h) * DK + 4 * kc;
             kraw[i] = *reinterpret_cast<const uint2 *>(kp + base);
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t keep = keep_mask(rg + 8 * i < len);
+            const uint32_t keep = keep_mask(8 * rg + i < len);
             kraw[i].x &= keep;
             kraw[i].y &= keep;
             if constexpr (GATE == KDA_GATE_RAW) {
@@ -522,7 +525,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int t = rg + 8 * i;
+            const int t = 8 * rg + i;
             const float4 k4 = make_float4(__uint_as_float(kraw[i].x << 16), __uint_as_float(kraw[i].x & 0xffff0000u),
                                           __uint_as_float(kraw[i].y << 16), __uint_as_float(kraw[i].y & 0xffff0000u));
             // the row's 1 / norm (every lane of the 32-lane row group holds it;
@@ -530,15 +533,52 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             const float rn = norm ? __builtin_amdgcn_rsqf(group_sum32(dot4(k4, k4)) + 1e-6f) : 1.0f;
             *reinterpret_cast<float4 *>(&sm.u.early.K[t][4 * kc]) =
                 make_float4(k4.x * rn, k4.y * rn, k4.z * rn, k4.w * rn);
-            *reinterpret_cast<float4 *>(&sm.u.early.G[t][4 * kc]) =
-                make_float4(g4[i].x * kLog2e, g4[i].y * kLog2e, g4[i].z * kLog2e, g4[i].w * kLog2e);
         }
+        // S2, the in-chunk cumsum of the log2 decay: this lane's eight rows in
+        // registers, then the row groups before it: its half-wave partner
+        // (rg - 1, for odd rg) by a lane exchange, earlier waves' pairs
+        // through LDS
+        float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            run.x += g4[i].x * kLog2e;
+            run.y += g4[i].y * kLog2e;
+            run.z += g4[i].z * kLog2e;
+            run.w += g4[i].w * kLog2e;
+            gcum[i] = run;
+        }
+        const float4 other = make_float4(__shfl_xor(run.x, 32), __shfl_xor(run.y, 32), __shfl_xor(run.z, 32),
+                                         __shfl_xor(run.w, 32));
+        const bool odd = (rg & 1) != 0;
+        if (odd) {
+            *reinterpret_cast<float4 *>(&sm.gsum[wave][4 * kc]) =
+                make_float4(other.x + run.x, other.y + run.y, other.z + run.z, other.w + run.w);
+        }
+        gprev = odd ? other : make_float4(0.f, 0.f, 0.f, 0.f);
         if (tid < BT) {
             float b = braw;
             if constexpr (GATE == KDA_GATE_RAW) {
                 b = __builtin_amdgcn_rcpf(1.0f + __expf(-b));
             }
             sm.beta[tid] = tid < len ? b : 0.f;
+        }
+    }
+    lds_barrier();
+    {
+        // the cumsum rows of this lane: its own prefix, the earlier waves'
+        // pair totals, and its partner's total
+        float4 add = gprev;
+        for (int w2 = 0; w2 < wave; ++w2) {
+            const float4 p4 = *reinterpret_cast<const float4 *>(&sm.gsum[w2][4 * kc]);
+            add.x += p4.x;
+            add.y += p4.y;
+            add.z += p4.z;
+            add.w += p4.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            *reinterpret_cast<float4 *>(&sm.u.early.G[8 * rg + i][4 * kc]) =
+                make_float4(gcum[i].x + add.x, gcum[i].y + add.y, gcum[i].z + add.z, gcum[i].w + add.w);
         }
     }
     if (norm) {
@@ -561,29 +601,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             if (gq == 0) {
                 sm.u.early.qss[sh][16 * (ii == 0 ? IA : 3 - IA) + r] = ss;
             }
-        }
-    }
-    lds_barrier();
-
-    // ---- S2: in-chunk cumsum of the log2 decay, per channel -----------------
-    {
-        const int ch = tid & 127;
-        const int half = tid >> 7;
-        float vals[32];
-        float run = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            run += sm.u.early.G[half * 32 + i][ch];
-            vals[i] = run;
-        }
-        if (half == 0) {
-            sm.carry[ch] = run;
-        }
-        lds_barrier();
-        const float add = half ? sm.carry[ch] : 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            sm.u.early.G[half * 32 + i][ch] = vals[i] + add;
         }
     }
     lds_barrier();
