@@ -310,7 +310,7 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
 // ---------------------------------------------------------------------------
 // K1: per (chunk, head) intra-chunk work.
 //
-// 67 KiB of LDS (two workgroups per CU, which its registers allow; at three,
+// 69 KiB of LDS (two workgroups per CU, which its registers allow; at three,
 // forced, it ran no faster). The chunk's k, g, beta and each wave's q rows
 // are loaded up front (v is not read here). k is normalized once and kept
 // in fp32, so every operand built from it reads ready values; the decay is
