@@ -96,11 +96,20 @@ constexpr int kOffSc = kOffGl + DK * 4;           // fp32 scale block [128], ind
 constexpr int kRecBytes = kOffSc + 512;           // 56320
 // Scale block: 2^-shift of each fp16 fragment group, and the bound the scan
 // derives y's scale from (|y| <= max|v| + kel1 max|S|).
-constexpr int kScKe = 0;     // [16] e^G k fragment (mt, s): mt * 4 + s (equal over s)
+constexpr int kScKe = 0;     // [16] e^G k fragment (mt, s): mt * 4 + s (equal within s = 0, 1 and s = 2, 3)
 constexpr int kScQg = 16;    // [16] q e^G fragment (mt, s) (equal within s = 0, 1 and s = 2, 3)
 constexpr int kScKd = 32;    // [8]  (T^T kd)^T row tile mk (both token slices)
 constexpr int kScAq = 40;    // [4]  Aqk T row tile mt (both token slices)
-constexpr int kScKel1 = 48;  // [4]  max over the rows t of tile mt of sum_k |(e^G k)[t][k]|
+constexpr int kScKel1 = 48;  // [8]  4 h + mt: max over the rows t of tile mt of the sum of
+                             //      |(e^G k)[t][k]| over channel half h (k in [64h, 64h + 64))
+// max over a chunk's rows t of sum_k |(e^G k)[t][k]|, bounded from above by
+// the two channel halves' maxima of each row tile
+__device__ __forceinline__ float kel1_bound(const float *sc) {
+    const float4 h0 = *reinterpret_cast<const float4 *>(sc + kScKel1);
+    const float4 h1 = *reinterpret_cast<const float4 *>(sc + kScKel1 + 4);
+    return fmaxf(fmaxf(h0.x + h1.x, h0.y + h1.y), fmaxf(h0.z + h1.z, h0.w + h1.w));
+}
+
 // Track record of one (sequence, head): operands of the state after r < len
 // tokens of the chunk holding the tracked position.
 constexpr int kTrOffKd = 0;                       // (T^T kd_r)^T fp16, scaled per row tile mk
@@ -664,6 +673,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
         bf16x8 Rh[2], Qh[2], Ql[2];
         float qg[2][8];  // q e^G of this half's two slices: one record scale
+        float ke[2][8];  // e^G k of the same rows and channels: one record scale
+        float l1 = 0.f;  // this lane's share of the row's sum of |e^G k| over the half
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
             const int s = 2 * sh + sl;
@@ -673,16 +684,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float ex = ex2(fminf(gg[e] - anc[sl][e], kMaxExp2));
+                const float eg = ex2(gg[e]);
                 const float qn = qv[sl][e] * qscale;
                 rv[e] = kk[e] * ex;
                 qa[e] = qn * ex;
-                qg[sl][e] = qn * ex2(gg[e]);
+                qg[sl][e] = qn * eg;
+                ke[sl][e] = kk[e] * eg;
+                l1 += fabsf(ke[sl][e]);
             }
             Rh[sl] = to_bf16x8(rv);
             split_bf16x8(qa, Qh[sl], Ql[sl]);
         }
-        store_frags_f16<2>(rec, kOffQg, I * 4 + 2 * sh, reinterpret_cast<float *>(rec + kOffSc) + kScQg + I * 4 + 2 * sh,
-                           lane, qg, 2);
+        float *sc = reinterpret_cast<float *>(rec + kOffSc);
+        store_frags_f16<2>(rec, kOffQg, I * 4 + 2 * sh, sc + kScQg + I * 4 + 2 * sh, lane, qg, 2);
+        // e^G k: the A fragments of row tile I, slices 2sh and 2sh+1, for the
+        // scan's (e^G k) S; and this half's max over the tile's rows of
+        // sum_k |e^G k|, which the scan adds to the other half's to bound that
+        // product with max |S|
+        store_frags_f16<2>(rec, kOffKe, I * 4 + 2 * sh, sc + kScKe + I * 4 + 2 * sh, lane, ke, 2);
+        l1 += __shfl_xor(l1, 16);
+        l1 += __shfl_xor(l1, 32);
+        l1 = wave_max(l1);
+        if (lane == 0) {
+            sc[kScKel1 + 4 * sh + I] = l1;
+        }
         // pairs (I, J), J <= I, over this half's channels
 #pragma unroll
         for (int J = 0; J < (ii == 0 ? 4 : 2); ++J) {
@@ -806,33 +831,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             if (tid < DK) {
                 reinterpret_cast<float *>(tr + kTrOffGl)[tid] = ex2(sm.u.early.G[rr - 1][tid]);
             }
-        }
-    }
-    // e^G k fragments (A, row tile mt = wave, channel slices 0..3) for the
-    // scan's (e^G k) S, one scale per row tile; kel1 = max over the tile's
-    // rows of sum_k |e^G k| bounds that product with max |S|.
-    {
-        const int row = 16 * wave + r;
-        float x[4][8];
-        float l1 = 0.f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            float kk[8], gg[8];
-            load_k8(row, s, kk);
-            load_g8(row, s, gg);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                x[s][e] = kk[e] * ex2(gg[e]);
-                l1 += fabsf(x[s][e]);
-            }
-        }
-        l1 += __shfl_xor(l1, 16);
-        l1 += __shfl_xor(l1, 32);
-        l1 = wave_max(l1);
-        float *sc = reinterpret_cast<float *>(rec + kOffSc);
-        store_frags_f16<4>(rec, kOffKe, wave * 4, sc + kScKe + wave * 4, lane, x, 4);
-        if (lane == 0) {
-            sc[kScKel1 + wave] = l1;
         }
     }
     lds_barrier();  // G and K are dead from here on
@@ -1376,8 +1374,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[j & 1][0]);
             op.vmax = fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w));
             op.kesc = *reinterpret_cast<const float4 *>(sc + kScKe + 4 * wr);
-            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScKel1);
-            op.kel1 = fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w));
+            op.kel1 = kel1_bound(sc);
         };
         auto step = [&](int j) {
             const int p = j & 1;
@@ -1568,11 +1565,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             const char *st = sm.stg[p];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
             const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[p][0]);
-            const float4 wl = *reinterpret_cast<const float4 *>(sc + kScKel1);
             const float4 sx = *reinterpret_cast<const float4 *>(&sm.smax[p][0]);
             const int sv = f16_shift(fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w)) +
-                                     fmaxf(fmaxf(wl.x, wl.y), fmaxf(wl.z, wl.w)) *
-                                         fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
+                                     kel1_bound(sc) * fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
             const float f = sc[kScAq + wr] * ldexpf(1.f, -sv);
             // rows [16wr, 16wr+16) meet tokens >= 32 only for wr >= 2
             const f16x8 aq0 = stage_frag(st, kStAq + aq_frag(wr, 0), lane);
