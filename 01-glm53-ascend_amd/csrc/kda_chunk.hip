@@ -213,7 +213,15 @@ __device__ __forceinline__ void split_f16x8(const float x[8], int sh, f16x8 &hi,
     for (int p = 0; p < 4; ++p) {
         const f32x2_t xs = {ldexpf(x[2 * p], sh), ldexpf(x[2 * p + 1], sh)};
         const f16x2_t h = __builtin_convertvector(xs, f16x2_t);
-        const f16x2_t l = __builtin_convertvector(xs - __builtin_convertvector(h, f32x2_t), f16x2_t);
+        // xs - hi, exact, with hi read as fp16 from its half of the packed pair
+        const uint32_t hp = __builtin_bit_cast(uint32_t, h);
+        float d0, d1;
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,0] op_sel_hi:[0,0,1]"
+            : "=v"(d0) : "v"(xs[0]), "v"(hp));
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+            : "=v"(d1) : "v"(xs[1]), "v"(hp));
+        const f32x2_t ds = {d0, d1};
+        const f16x2_t l = __builtin_convertvector(ds, f16x2_t);
         hi[2 * p] = h[0];
         hi[2 * p + 1] = h[1];
         lo[2 * p] = l[0];
