@@ -271,6 +271,38 @@ __device__ __forceinline__ void store_frags_f16(char *base, int off, int idx, fl
     }
 }
 
+// store_frags_f16 for values given as x * 2^ex[t], with t = 2f + (e >= 4) the
+// 16-row tile of element e of fragment f: the exponents join the fragment's
+// own shift (one ldexp per value; power-of-two factors change no bits).
+template <int NF>
+__device__ __forceinline__ void store_frags_f16_exp(char *base, int off, int idx, float *sc, int lane,
+                                                    const float (&x)[NF][8], const int (&ex)[2 * NF]) {
+    float m = 0.f;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        float m0 = 0.f, m1 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            m0 = fmaxf(m0, fabsf(x[f][e]));
+            m1 = fmaxf(m1, fabsf(x[f][4 + e]));
+        }
+        m = fmaxf(m, fmaxf(ldexpf(m0, ex[2 * f]), ldexpf(m1, ex[2 * f + 1])));
+    }
+    const int sh = f16_shift(wave_max(m));
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        f16x8 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h[e] = static_cast<_Float16>(ldexpf(x[f][e], sh + ex[2 * f + (e >> 2)]));
+        }
+        reinterpret_cast<u32x4 *>(base + off)[(idx + f) * 64 + lane] = as_u32x4(h);
+    }
+    if (lane == 0) {
+        sc[0] = ldexpf(1.f, -sh);
+    }
+}
+
 
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
 // accesses, not for its outstanding global loads (a full __syncthreads() also
@@ -374,7 +406,7 @@ struct PrepShared {
             // Lower triangle with the diagonal: Aqk[i][j] (j <= i).
             float LT[BT][kPadX];
             u32x4 TT[4][2][2][64];  // T^T A fragments (row tile, token slice, hi / lo) (S6)
-            float ttinv[4];         // their 2^-shift per row tile
+            int ttsh[4];            // their power-of-two shift per row tile
         } mid;
     } u;
     float beta[BT];
@@ -760,10 +792,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
     // kd[t][16mk + r] = k_t e^(G_last - G_t) for the rows t = 32s + kperm(gq, e)
     // (B fragments of T^T kd, mk = 2 wave + tt), fp16 hi + lo with one
-    // power-of-two scale per mk; S6 uses them from registers.
+    // power-of-two scale 2^-shift per mk; S6 uses them from registers.
     u32x4 kdh[2][2], kdl[2][2];
-    float kdinv[2];
-    auto to_frags = [&](const float (&x)[2][8], u32x4 (&fh)[2], u32x4 (&fl)[2], float &inv) {
+    int kdsh[2];
+    auto to_frags = [&](const float (&x)[2][8], u32x4 (&fh)[2], u32x4 (&fl)[2], int &shift) {
         float m = 0.f;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -780,7 +812,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             fh[s] = as_u32x4(hi);
             fl[s] = as_u32x4(lo);
         }
-        inv = ldexpf(1.f, -sh);
+        shift = sh;
     };
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -798,7 +830,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 x[s][e] = kr[e] * ex2(gl - sm.u.early.G[t][k]);
             }
         }
-        to_frags(x, kdh[tt], kdl[tt], kdinv[tt]);
+        to_frags(x, kdh[tt], kdl[tt], kdsh[tt]);
     }
     if (tid < DK) {
         reinterpret_cast<float *>(rec + kOffGl)[tid] = ex2(sm.u.early.G[BT - 1][tid]);
@@ -810,7 +842,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     bool tracked = false;
     char *tr = nullptr;
     u32x4 kth[2][2], ktl[2][2];
-    float ktinv[2] = {0.f, 0.f};
+    int ktsh[2] = {0, 0};
     if (a.track_indices != nullptr) {
         const int ts = a.track_indices[n];
         const int tl = a.track_lens[n];
@@ -834,7 +866,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                         x[s][e] = t < rr ? kr[e] * ex2(gr - sm.u.early.G[t][k]) : 0.f;
                     }
                 }
-                to_frags(x, kth[tt], ktl[tt], ktinv[tt]);
+                to_frags(x, kth[tt], ktl[tt], ktsh[tt]);
             }
             if (tid < DK) {
                 reinterpret_cast<float *>(tr + kTrOffGl)[tid] = ex2(sm.u.early.G[rr - 1][tid]);
@@ -1027,20 +1059,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             sm.u.mid.TT[wave][s][1][lane] = as_u32x4(lo);
         }
         if (lane == 0) {
-            sm.u.mid.ttinv[wave] = ldexpf(1.f, -sh);
+            sm.u.mid.ttsh[wave] = sh;
         }
     }
     lds_barrier();
-    float ttinv[4];
+    int ttsh[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-        ttinv[tt] = sm.u.mid.ttinv[tt];
+        ttsh[tt] = sm.u.mid.ttsh[tt];
     }
     // T^T B (rows t, B's columns) for the B fragments bh[s] + bl[s] of a
-    // 16-column block (three passes: T hi B hi, T hi B lo, T lo B hi), K =
-    // token slices s >= tt / 2 (T^T is zero below), scaled; the four row
-    // tiles land in x[2][8] in A-fragment order
-    auto ttb = [&](const u32x4 (&bh)[2], const u32x4 (&bl)[2], float scale, float (&x)[2][8], int tmax) {
+    // 16-column block, B scaled by 2^bsh (three passes: T hi B hi, T hi B lo,
+    // T lo B hi), K = token slices s >= tt / 2 (T^T is zero below); the four
+    // row tiles land unscaled in x[2][8] in A-fragment order, tile tt's
+    // exponent in ex[tt]
+    auto ttb = [&](const u32x4 (&bh)[2], const u32x4 (&bl)[2], int bsh, float (&x)[2][8], int tmax,
+                   int (&ex)[4]) {
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
             if (tt > tmax) {
@@ -1054,10 +1088,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 acc = mfma(th, as_f16x8(bl[s]), acc);
                 acc = mfma(as_f16x8(sm.u.mid.TT[tt][s][1][lane]), as_f16x8(bh[s]), acc);
             }
-            const float f = ttinv[tt] * scale;
+            ex[tt] = -(ttsh[tt] + bsh);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                x[tt >> 1][4 * (tt & 1) + i] = acc[i] * f;
+                x[tt >> 1][4 * (tt & 1) + i] = acc[i];
             }
         }
     };
@@ -1066,16 +1100,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int tt = 0; tt < 2; ++tt) {
         const int mk = 2 * wave + tt;
         float x[2][8];
-        ttb(kdh[tt], kdl[tt], kdinv[tt], x, 3);
-        store_frags_f16<2>(rec, kOffKd, mk * 2, sc + kScKd + mk, lane, x);
+        int ex[4];
+        ttb(kdh[tt], kdl[tt], kdsh[tt], x, 3, ex);
+        store_frags_f16_exp<2>(rec, kOffKd, mk * 2, sc + kScKd + mk, lane, x, ex);
     }
     if (tracked) {
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int mk = 2 * wave + tt;
             float x[2][8];
-            ttb(kth[tt], ktl[tt], ktinv[tt], x, 3);
-            store_frags_f16<2>(tr, kTrOffKd, mk * 2, reinterpret_cast<float *>(tr + kTrOffSc) + mk, lane, x);
+            int ex[4];
+            ttb(kth[tt], ktl[tt], ktsh[tt], x, 3, ex);
+            store_frags_f16_exp<2>(tr, kTrOffKd, mk * 2, reinterpret_cast<float *>(tr + kTrOffSc) + mk, lane, x,
+                                   ex);
         }
     }
     {
@@ -1096,8 +1133,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             }
         }
         u32x4 aqh[2], aql[2];
-        float aqinv;
-        to_frags(ax, aqh, aql, aqinv);
+        int aqsh;
+        to_frags(ax, aqh, aql, aqsh);
         float x[2][8];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -1106,7 +1143,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 x[s][e] = 0.f;
             }
         }
-        ttb(aqh, aql, aqinv, x, wave);
+        int ex[4] = {0, 0, 0, 0};
+        ttb(aqh, aql, aqsh, x, wave, ex);
         float *asc = sc + kScAq + wave;
         if (wave < 2) {
             float x1[1][8];
@@ -1114,9 +1152,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             for (int e = 0; e < 8; ++e) {
                 x1[0][e] = x[0][e];
             }
-            store_frags_f16<1>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x1);
+            const int ex1[2] = {ex[0], ex[1]};
+            store_frags_f16_exp<1>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x1, ex1);
         } else {
-            store_frags_f16<2>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x);
+            store_frags_f16_exp<2>(rec, kOffAq, aq_frag(wave, 0), asc, lane, x, ex);
         }
     }
 }
