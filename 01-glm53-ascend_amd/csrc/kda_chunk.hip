@@ -489,9 +489,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // widened q: 8 channels {32s + kperm(gq, e)} of slice s = 2 sh + q2, the
     // padding rows zeroed (loaded from a row clamped into the chunk)
     auto q8 = [&](int ii, int q2, float x[8]) {
-        const uint32_t keep = keep_mask(16 * (ii == 0 ? IA : 3 - IA) + r < len);
-        const uint2 q0 = make_uint2(qraw[ii][q2][0].x & keep, qraw[ii][q2][0].y & keep);
-        const uint2 q1 = make_uint2(qraw[ii][q2][1].x & keep, qraw[ii][q2][1].y & keep);
+        uint2 q0 = qraw[ii][q2][0];
+        uint2 q1 = qraw[ii][q2][1];
+        if (len < BT) {
+            const uint32_t keep = keep_mask(16 * (ii == 0 ? IA : 3 - IA) + r < len);
+            q0 = make_uint2(q0.x & keep, q0.y & keep);
+            q1 = make_uint2(q1.x & keep, q1.y & keep);
+        }
         x[0] = __uint_as_float(q0.x << 16);
         x[1] = __uint_as_float(q0.x & 0xffff0000u);
         x[2] = __uint_as_float(q0.y << 16);
@@ -553,12 +557,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 qraw[ii][q2][1] = *reinterpret_cast<const uint2 *>(row + 16 + 4 * gq);
             }
         }
+        if constexpr (GATE == KDA_GATE_RAW) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t keep = keep_mask(8 * rg + i < len);
-            kraw[i].x &= keep;
-            kraw[i].y &= keep;
-            if constexpr (GATE == KDA_GATE_RAW) {
+            for (int i = 0; i < 8; ++i) {
                 const float4 av = g4[i];
                 const float lb = a.lower_bound;
                 // lb * sigmoid(x), the reciprocal as v_rcp_f32 (within 1 ulp)
@@ -567,10 +568,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 g4[i].z = lb * __builtin_amdgcn_rcpf(1.0f + __expf(-(expA * (av.z + dtb.z))));
                 g4[i].w = lb * __builtin_amdgcn_rcpf(1.0f + __expf(-(expA * (av.w + dtb.w))));
             }
-            g4[i].x = __uint_as_float(__float_as_uint(g4[i].x) & keep);
-            g4[i].y = __uint_as_float(__float_as_uint(g4[i].y) & keep);
-            g4[i].z = __uint_as_float(__float_as_uint(g4[i].z) & keep);
-            g4[i].w = __uint_as_float(__float_as_uint(g4[i].w) & keep);
+        }
+        if (len < BT) {  // a partial chunk: its padding rows' k and g become zero
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t keep = keep_mask(8 * rg + i < len);
+                kraw[i].x &= keep;
+                kraw[i].y &= keep;
+                g4[i].x = __uint_as_float(__float_as_uint(g4[i].x) & keep);
+                g4[i].y = __uint_as_float(__float_as_uint(g4[i].y) & keep);
+                g4[i].z = __uint_as_float(__float_as_uint(g4[i].z) & keep);
+                g4[i].w = __uint_as_float(__float_as_uint(g4[i].w) & keep);
+            }
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -763,9 +772,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 float kk[8], gg[8], cv[8];
                 load_k8(rj, s, kk);
                 load_g8(rj, s, gg);
+                // blocks 0 and 1 against the upper row block I = IA >= 2 are
+                // earlier blocks: anchor - G_j <= 0 (g <= 0), no clamp needed
+                const bool earlier = ii == 0 && J < 2;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    cv[e] = kk[e] * ex2(fminf(anc[sl][e] - gg[e], kMaxExp2));
+                    const float d = anc[sl][e] - gg[e];
+                    cv[e] = kk[e] * ex2(earlier ? d : fminf(d, kMaxExp2));
                 }
                 bf16x8 Ch, Cl;
                 split_bf16x8(cv, Ch, Cl);
