@@ -248,6 +248,25 @@ __device__ __forceinline__ float wave_max(float x) {
     return fmaxf(a, b);
 }
 
+// Largest value over the wave for nonnegative x (magnitudes and sums of
+// magnitudes): their bit patterns order as the values do, so the reduction runs
+// on them as unsigned integers (zero, what a lane without a source would
+// read, is the identity), each DPP step one fused max and the cross-row tail
+// on scalars.
+__device__ __forceinline__ float wave_max_mag(float x) {
+    uint32_t u = __float_as_uint(x);
+    u = max(u, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(u), kDppQuadXor1, 0xf, 0xf, true)));
+    u = max(u, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(u), kDppQuadXor2, 0xf, 0xf, true)));
+    u = max(u, static_cast<uint32_t>(
+                   __builtin_amdgcn_mov_dpp(static_cast<int>(u), kDppRowHalfMirror, 0xf, 0xf, true)));
+    u = max(u, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(u), kDppRowMirror, 0xf, 0xf, true)));
+    const uint32_t a = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 0)),
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 16)));
+    const uint32_t b = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 32)),
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 48)));
+    return __uint_as_float(max(a, b));
+}
+
 // One wave stores NF consecutive fp16 fragments with one shared scale, and
 // writes the inverse scale to sc[0 .. nsc).
 template <int NF>
@@ -261,7 +280,7 @@ __device__ __forceinline__ void store_frags_f16(char *base, int off, int idx, fl
             m = fmaxf(m, fabsf(x[f][e]));
         }
     }
-    const int sh = f16_shift(wave_max(m));
+    const int sh = f16_shift(wave_max_mag(m));
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         reinterpret_cast<u32x4 *>(base + off)[(idx + f) * 64 + lane] = as_u32x4(to_f16x8(x[f], sh));
@@ -288,7 +307,7 @@ __device__ __forceinline__ void store_frags_f16_exp(char *base, int off, int idx
         }
         m = fmaxf(m, fmaxf(ldexpf(m0, ex[2 * f]), ldexpf(m1, ex[2 * f + 1])));
     }
-    const int sh = f16_shift(wave_max(m));
+    const int sh = f16_shift(wave_max_mag(m));
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         f16x8 h;
@@ -753,7 +772,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         store_frags_f16<2>(rec, kOffKe, I * 4 + 2 * sh, sc + kScKe + I * 4 + 2 * sh, lane, ke, 2);
         l1 += __shfl_xor(l1, 16);
         l1 += __shfl_xor(l1, 32);
-        l1 = wave_max(l1);
+        l1 = wave_max_mag(l1);
         if (lane == 0) {
             sc[kScKel1 + 4 * sh + I] = l1;
         }
@@ -817,7 +836,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 m = fmaxf(m, fabsf(x[s][e]));
             }
         }
-        const int sh = f16_shift(wave_max(m));
+        const int sh = f16_shift(wave_max_mag(m));
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             f16x8 hi, lo;
@@ -1063,7 +1082,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 m = fmaxf(m, fabsf(tx[s][e]));
             }
         }
-        const int sh = f16_shift(wave_max(m));
+        const int sh = f16_shift(wave_max_mag(m));
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             f16x8 hi, lo;
@@ -1458,7 +1477,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                         }
                     }
                 }
-                m = wave_max(m);
+                m = wave_max_mag(m);
                 const int ssh = f16_shift(m);
 #pragma unroll
                 for (int ct = 0; ct < NT; ++ct) {
@@ -1813,7 +1832,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 m = max(m, max(max(V[k].x & 0x7fffu, (V[k].x >> 16) & 0x7fffu),
                                max(V[k].y & 0x7fffu, (V[k].y >> 16) & 0x7fffu)));
             }
-            const float mf = wave_max(__uint_as_float(m << 16));
+            const float mf = wave_max_mag(__uint_as_float(m << 16));
             if (lane == 0) {
                 sm.vmax[par][wl] = mf;
             }
