@@ -102,12 +102,21 @@ constexpr int kScKd = 32;    // [8]  (T^T kd)^T row tile mk (both token slices)
 constexpr int kScAq = 40;    // [4]  Aqk T row tile mt (both token slices)
 constexpr int kScKel1 = 48;  // [8]  4 h + mt: max over the rows t of tile mt of the sum of
                              //      |(e^G k)[t][k]| over channel half h (k in [64h, 64h + 64))
+// Largest of four nonnegative values (magnitudes), compared as their bit
+// patterns: no quieting of the operands as fmaxf needs for values it did not
+// produce itself.
+__device__ __forceinline__ float max4_mag(float a, float b, float c, float d) {
+    return __uint_as_float(max(max(__float_as_uint(a), __float_as_uint(b)),
+                               max(__float_as_uint(c), __float_as_uint(d))));
+}
+__device__ __forceinline__ float max4_mag(float4 v) { return max4_mag(v.x, v.y, v.z, v.w); }
+
 // max over a chunk's rows t of sum_k |(e^G k)[t][k]|, bounded from above by
 // the two channel halves' maxima of each row tile
 __device__ __forceinline__ float kel1_bound(const float *sc) {
     const float4 h0 = *reinterpret_cast<const float4 *>(sc + kScKel1);
     const float4 h1 = *reinterpret_cast<const float4 *>(sc + kScKel1 + 4);
-    return fmaxf(fmaxf(h0.x + h1.x, h0.y + h1.y), fmaxf(h0.z + h1.z, h0.w + h1.w));
+    return max4_mag(h0.x + h1.x, h0.y + h1.y, h0.z + h1.z, h0.w + h1.w);
 }
 
 // Track record of one (sequence, head): operands of the state after r < len
@@ -1451,7 +1460,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
             const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[j & 1][0]);
-            op.vmax = fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w));
+            op.vmax = max4_mag(um);
             op.kesc = *reinterpret_cast<const float4 *>(sc + kScKe + 4 * wr);
             op.kel1 = kel1_bound(sc);
         };
@@ -1503,7 +1512,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             // j are read behind the first tile's S fragments.
             const float4 sx = *reinterpret_cast<const float4 *>(&sm.smax[p][0]);
             const float4 ss = *reinterpret_cast<const float4 *>(&sm.sscale[p][0]);
-            const int sv = f16_shift(ob.vmax + ob.kel1 * fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
+            const int sv = f16_shift(ob.vmax + ob.kel1 * max4_mag(sx));
             const float inv_v = ldexpf(1.f, -sv);
             const float fw[4] = {ob.kesc.x * ss.x, ob.kesc.y * ss.y, ob.kesc.z * ss.z, ob.kesc.w * ss.w};
             f16x8 Kd[2][2];
@@ -1645,8 +1654,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
             const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[p][0]);
             const float4 sx = *reinterpret_cast<const float4 *>(&sm.smax[p][0]);
-            const int sv = f16_shift(fmaxf(fmaxf(um.x, um.y), fmaxf(um.z, um.w)) +
-                                     kel1_bound(sc) * fmaxf(fmaxf(sx.x, sx.y), fmaxf(sx.z, sx.w)));
+            const int sv = f16_shift(max4_mag(um) + kel1_bound(sc) * max4_mag(sx));
             const float f = sc[kScAq + wr] * ldexpf(1.f, -sv);
             // rows [16wr, 16wr+16) meet tokens >= 32 only for wr >= 2
             const f16x8 aq0 = stage_frag(st, kStAq + aq_frag(wr, 0), lane);
