@@ -1735,10 +1735,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             if (j > j0) {
                 aqk_y(j - 1);
             }
-            lds_barrier();  // B2(j)
-            if (j > j0) {
-                finish(j - 1);
-            }
+            f32x4 Pn[NT];
             const float4 ss = *reinterpret_cast<const float4 *>(&sm.sscale[p][0]);
             const float fq[4] = {cur.qsc.x * ss.x, cur.qsc.y * ss.y, cur.qsc.z * ss.z, cur.qsc.w * ss.w};
 #pragma unroll
@@ -1755,8 +1752,16 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                     for (int s = 0; s < 4; ++s) {
                         x += fq[s] * acc[s][i];
                     }
-                    P[ct][i] = x;
+                    Pn[ct][i] = x;
                 }
+            }
+            lds_barrier();  // B2(j)
+            if (j > j0) {
+                finish(j - 1);
+            }
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) {
+                P[ct] = Pn[ct];
             }
         };
         OpsO opA, opB;
