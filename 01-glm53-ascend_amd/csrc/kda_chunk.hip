@@ -1210,8 +1210,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 //                     and run the recurrence: publish S_j, y_j = v - (e^G k)
 //                     S_j, publish y_j, S_{j+1} = e^(G_last) S_j +
 //                     (T^T kd)^T y_j;
-//   output waves 4-7  own token rows [16o, 16o+16): (q e^G) S_j between B2(j)
-//                     and B1(j+1), (Aqk T) y_j between B1(j+1) and B2(j+1)
+//   output waves 4-7  own token rows [16o, 16o+16): (q e^G) S_j between B1(j)
+//                     and B2(j), (Aqk T) y_j between B1(j+1) and B2(j+1)
 //                     (Aqk T from the stage, y_j from its LDS hand-over),
 //                     then o_j = the sum and its store after B2(j+1); they
 //                     load their q e^G fragments themselves, a chunk ahead;
@@ -1724,10 +1724,10 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
             op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 4 * (kScQg + 4 * wr));
         };
-        // Iteration j: [B1(j)] load chunk j+1 into `other` and form A of
-        // chunk j-1, [B2(j)] finish chunk j-1, then P = (q e^G) S_j from
-        // `cur`: fp16 q e^G against fp16 S_j, one product per slice, then
-        // scaled.
+        // Iteration j: [B1(j)] load chunk j+1 into `other`, form A of chunk
+        // j-1 and P = (q e^G) S_j from `cur` (fp16 q e^G against fp16 S_j,
+        // one product per slice, then scaled; S_j's buffer is rewritten only
+        // after B1(j+1)), [B2(j)] finish chunk j-1 (its P and A), keep P_j.
         auto iter = [&](const OpsO &cur, OpsO &other, int j) {
             const int p = j & 1;
             lds_barrier();  // B1(j)
