@@ -155,6 +155,16 @@ at::Tensor run_chunk(const char *op, KdaChunkArgs &args, const at::Tensor &q);
 // runs in the chunked form (measured: 1024 tokens on 4 heads take ~1 ms
 // token by token, a few tens of microseconds in 64-token chunks).
 constexpr int64_t kChunkRouteTokensPerRequest = 128;
+// ... but only inside the chunk kernels' exponent envelope: with raw gates
+// g >= lower_bound per token, so 8 tokens decay by at most 8 |lower_bound|
+// nat, which must stay below 2^126 (87.3 nat); a lower bound under this
+// keeps the token loop, which has no such limit.
+constexpr double kChunkRouteMinLowerBound = -10.9;
+// ... and with a bounded workspace: the token loop allocates nothing beyond
+// the output, so the chunked route takes at most this much scratch. A single
+// sequence needing more runs in windows of what this holds; several
+// sequences needing more, or an allocation that fails, keep the token loop.
+constexpr size_t kChunkRouteMaxWorkspace = size_t{512} << 20;
 
 // ---------------------------------------------------------------------------
 // kda_varlen_recurrent
@@ -245,11 +255,28 @@ at::Tensor varlen_recurrent_impl(const char *op, const at::Tensor &A_log, const 
     }
     const PoolRef pr = pool_ref(pool);
 
-    if (prefill && D == 128 && T >= kChunkRouteTokensPerRequest * N) {
-        // Long prefill: the chunked form of the same recurrence (64-token
-        // chunks on MFMA, within the tolerance contract of the token loop)
-        // instead of a serial pass over every token. Same slot, padding,
-        // tracking and uncovered-token rules.
+    // Long prefill: the chunked form of the same recurrence (64-token chunks
+    // on MFMA, within the tolerance contract of the token loop) instead of a
+    // serial pass over every token. Same slot, padding, tracking and
+    // uncovered-token rules.
+    size_t route_ws = 0;
+    if (prefill && D == 128 && T >= kChunkRouteTokensPerRequest * N &&
+        lower_bound >= kChunkRouteMinLowerBound) {
+        route_ws = kda_chunk_workspace_bytes(static_cast<int32_t>(T), static_cast<int32_t>(N),
+                                             static_cast<int32_t>(H), static_cast<int32_t>(D));
+        if (route_ws > kChunkRouteMaxWorkspace) {
+            route_ws = N == 1 ? kChunkRouteMaxWorkspace : 0;
+        }
+    }
+    std::optional<at::Tensor> route_buf;
+    if (route_ws > 0) {
+        try {
+            route_buf = at::empty({static_cast<int64_t>(route_ws)}, q.options().dtype(at::kByte));
+        } catch (const c10::OutOfMemoryError &) {
+            route_buf.reset();  // the token loop needs no scratch
+        }
+    }
+    if (route_buf.has_value()) {
         KdaChunkArgs cargs{};
         cargs.q = q.data_ptr();
         cargs.k = k.data_ptr();
@@ -279,7 +306,7 @@ at::Tensor varlen_recurrent_impl(const char *op, const at::Tensor &A_log, const 
         cargs.v_dtype = KDA_BF16;
         cargs.gate_mode = KDA_GATE_RAW;
         cargs.qk_l2norm = 1;
-        run_chunk(op, cargs, q);
+        check_ok(kda_chunk_launch(&cargs, route_buf->data_ptr(), route_ws, stream_of(q)), op);
         return out;
     }
 

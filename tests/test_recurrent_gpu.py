@@ -548,3 +548,25 @@ def test_recurrent_no_tokens_tracks_initial_state(gpu_ops):
     assert torch.equal(got[5], torch.zeros_like(got[5])), "slot-0 request tracks a zero state"
     for s in (0, 1, 2, 3):
         assert torch.equal(got[s], case.pool[s]), f"slot {s} changed"
+
+
+@pytest.mark.parametrize("lower_bound,chunk_route", [(-12.0, False), (-10.0, True)])
+def test_prefill_route_respects_exponent_envelope(gpu_ops, lower_bound, chunk_route):
+    """A long raw-gate prefill runs the chunked kernels only while 8 tokens
+    of decay stay inside their exponent envelope (lower_bound >= -10.9); a
+    harsher bound keeps the token loop. The gate input is shifted so that
+    sigmoid saturates and g sits near 0.98 * lower_bound on every token
+    (8 tokens: about 94 nat at -12, beyond the envelope; 78 at -10)."""
+    case = C.raw_case(4, (200, 130), indices=[1, 2], slots=4, seed=1212,
+                      lower_bound=lower_bound)
+    case.a = (case.a.float() + 4.0).bfloat16()
+    out, pool = _run_raw(gpu_ops, case, prefill=True)
+    ref_pool = C.clone_pool(case.pool)
+    ref = _oracle_raw(case, ref_pool)
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, f"lower_bound {lower_bound} output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, f"lower_bound {lower_bound} state")
+    pool_c = C.to_dev(case.pool, DEV)
+    out_c = gpu_ops.kda_varlen_chunk(prefill=True, **case.kwargs(DEV, pool=pool_c))
+    torch.cuda.synchronize()
+    same = torch.equal(out, out_c) and torch.equal(pool, pool_c)
+    assert same == chunk_route, "prefill took the wrong route"
