@@ -355,7 +355,80 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
         float beta;
         float v[NP];
     };
-    auto widen = [&](const TokenIn &in, Token &w) {
+    // Every row group of a workgroup needs the same per-channel decays, beta
+    // and norms of a token. With one vector per lane and row (EV == 1: the
+    // row groups' L lanes cover the D channels four apiece) and one or two
+    // tokens per sequence, the workgroup computes them once and shares them
+    // through LDS: the row groups of the waves before kNormWave each take one
+    // component of their lanes' vectors (rows groups 0-3: channels 4 kc + r),
+    // wave kNormWave forms the q norm (its even row groups) and the k norm
+    // (odd ones) with the same group sums every row group would use, and the
+    // next wave forms beta. Each value is the same expression of the same
+    // inputs as in the per-lane form, so the results are bitwise those of
+    // every row group computing everything itself; the raw decode's prologue
+    // (two expf and a division per channel) then runs once per (token,
+    // channel) in the workgroup instead of once per row group (8x fewer).
+    // Tokens alternate between two LDS sets, so one barrier per token
+    // separates the writes of token t + 2 from the reads of token t.
+    constexpr bool kShare = GATE != KDA_GATE_DECAY && TPS <= 2 && EV == 1;
+    constexpr int kNormWave = 4 / RPW;
+    static_assert(!kShare || (4 * L == D && kNormWave + 1 < 4), "roles of the shared prologue");
+    __shared__ float4 sh_dec[kShare ? 2 : 1][kShare ? L : 1];
+    __shared__ float sh_tok[kShare ? 2 : 1][4];
+    auto widen = [&](const TokenIn &in, Token &w, int t) {
+        if constexpr (kShare) {
+            const int par = t & 1;
+            w.q[0] = in.q[0].get();
+            w.k[0] = in.k[0].get();
+            const float4 gv = in.g[0].get();
+            if (wave < kNormWave) {
+                // this row group's channel 4 kc + r, r = rgw < 4
+                const int r = rgw;
+                const float x = r == 0 ? gv.x : r == 1 ? gv.y : r == 2 ? gv.z : gv.w;
+                float d;
+                if constexpr (GATE == KDA_GATE_RAW) {
+                    const float db = r == 0 ? dtb[0].x : r == 1 ? dtb[0].y : r == 2 ? dtb[0].z : dtb[0].w;
+                    d = dexp(a.lower_bound / (1.0f + dexp(-(expA * (x + db)))));
+                } else {
+                    d = dexp(x);
+                }
+                reinterpret_cast<float *>(&sh_dec[par][kc])[r] = d;
+            } else if (wave == kNormWave) {
+                if (norm) {
+                    const bool kr_group = (rgw & 1) != 0;
+                    float s = 0.f;
+                    s += kr_group ? dot4(w.k[0], w.k[0]) : dot4(w.q[0], w.q[0]);
+                    s = group_sum<L>(s);
+                    const float inv = 1.0f / sqrtf(s + 1e-6f);
+                    if (kc == 0 && rgw < 4 + 2) {
+                        sh_tok[par][kr_group ? 1 : 0] = kr_group ? inv : inv * a.scale;
+                    }
+                }
+            } else if (wave == kNormWave + 1) {
+                if (kc == 0 && (rgw & (RPW - 1)) == 0) {
+                    if constexpr (GATE == KDA_GATE_RAW) {
+                        sh_tok[par][2] = 1.0f / (1.0f + dexp(-in.b));
+                    } else {
+                        sh_tok[par][2] = in.b;
+                    }
+                }
+            }
+            __syncthreads();
+            w.dec[0] = sh_dec[par][kc];
+            w.beta = sh_tok[par][2];
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                w.v[p] = in.v.get(p);
+            }
+            float qsc = a.scale;
+            if (norm) {
+                qsc = sh_tok[par][0];
+                const float kr = sh_tok[par][1];
+                w.k[0] = make_float4(w.k[0].x * kr, w.k[0].y * kr, w.k[0].z * kr, w.k[0].w * kr);
+            }
+            w.q[0] = make_float4(w.q[0].x * qsc, w.q[0].y * qsc, w.q[0].z * qsc, w.q[0].w * qsc);
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < EV; ++j) {
             w.q[j] = in.q[j].get();
@@ -475,7 +548,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
             fetch(bos, in);
             for (int t = bos; t < eos; ++t) {
                 Token w;
-                widen(in, w);
+                widen(in, w, t);
                 fetch(t + 1 < eos ? t + 1 : t, in);
                 step(w, t);
             }
@@ -493,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(const KdaRecurrentA
                 fetch(t + 1, nxt);
             }
             Token w;
-            widen(cur, w);
+            widen(cur, w, t);
             step(w, t);
             cur = nxt;
         }
