@@ -52,7 +52,8 @@ def prepared_recurrent(
     Writes ``out`` and ``state`` in place for heads
     ``[head_offset, head_offset + 4)`` (the reference's four heads per
     launch, prepared_recurrent.cpp:629-634). ``state`` may be K-contiguous
-    (native, updated in place) or [K,V]-contiguous (updated through a copy).
+    (native) or [K,V]-contiguous (the reference's layout); either is read and
+    updated in place, with no pool-sized working copy.
     """
     return _OPS.prepared_recurrent(
         qn, kn, v, gdecay, beta, out, state, indices, starts,

@@ -219,11 +219,12 @@ print("CAPTURE-OK")
 
 
 def test_long_prefill_captured_before_any_eager_call(gpu_ops):
-    """A single long sequence eligible for the two-segment form, captured into
-    a graph as the process's first such call: the library has no side stream
-    yet and must not create one during a capture, so the captured call runs
-    the single-pass form. Runs in a fresh interpreter (this process has made
-    long calls already); every replay equals the eager result bitwise."""
+    """A single long sequence eligible for the pipelined segments, captured
+    into a graph as the process's first such call: the library has no side
+    stream yet and must not create one during a capture, so the captured call
+    runs the same segments one after another on the capturing stream. Runs in
+    a fresh interpreter (this process has made long calls already); every
+    replay equals the eager result bitwise."""
     import os
     import subprocess
     import sys
