@@ -33,12 +33,17 @@
 //                           output waves compute o one phase behind, four
 //                           loader waves stage the chain's operands and v in
 //                           LDS; S and y are exchanged through LDS.
+// A single long sequence on few heads, whose one scan would leave most CUs
+// idle, takes the affine form instead (chunk_affine_combine_kernel): K1 for
+// every chunk, then segment 0 scanned as usual while every later segment is
+// scanned from zero and from the identity at once, then a serial combine of
+// the segments' transitions and a parallel correction of their outputs.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16 / _f16 with fp32 accumulation. Inside K1,
 // operands whose rounding would break the tolerance contract are carried as
-// bf16 hi + lo pairs (x = hi + lo to ~2^-17) and multiplied in two or three
-// passes: Aqk (q split, then k split); Akk runs single-pass; T^T kd and
-// Aqk T take T, kd and Aqk as fp16 hi + lo pairs (~2^-22) in three passes.
+// bf16 hi + lo pairs (x = hi + lo to ~2^-17) and multiplied in three passes
+// (hi hi, hi lo, lo hi): Akk and Aqk; T^T kd and Aqk T take T, kd and Aqk
+// as fp16 hi + lo pairs (~2^-22) in three passes.
 // The record the scan reads holds every matrix operand as fp16 (11-bit
 // significands) with a power-of-two scale per fragment or row tile: e^G k,
 // q e^G, (T^T kd)^T and Aqk T. The scan meets them with S_j as fp16 (scaled
@@ -155,6 +160,30 @@ __host__ __device__ inline Layout layout(int T, int N, int H, int ring) {
     return L;
 }
 __host__ __device__ inline Layout layout(int T, int N, int H) { return layout(T, N, H, max_chunks(T, N)); }
+
+// The affine form of one sequence (P segments; see chunk_affine_combine_kernel)
+// keeps every chunk's record (the one-pass layout) and adds: the fp32
+// outputs of the later segments' zero-start and identity-start scans
+// ([T][H][V] each, indexed by token), the two scans' final states per later
+// segment and the true state at each later segment's start ([P-1][H][V][K]
+// each, K contiguous), and the two scans' tracked states ([H][V][K] each).
+struct AffLayout {
+    size_t out_zero, out_phi, fin_zero, fin_phi, start, trk_zero, trk_phi, total;
+};
+__host__ __device__ inline AffLayout aff_layout(int T, int H, int P) {
+    const size_t st = static_cast<size_t>(H) * DK * DK * 4;
+    const size_t ob = align256(static_cast<size_t>(T) * H * DK * 4);
+    AffLayout A;
+    A.out_zero = layout(T, 1, H).total;
+    A.out_phi = A.out_zero + ob;
+    A.fin_zero = A.out_phi + ob;
+    A.fin_phi = A.fin_zero + st * (P - 1);
+    A.start = A.fin_phi + st * (P - 1);
+    A.trk_zero = A.start + st * (P - 1);
+    A.trk_phi = A.trk_zero + st;
+    A.total = A.trk_phi + st;
+    return A;
+}
 
 __device__ __forceinline__ int kperm(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
 
@@ -447,16 +476,27 @@ static_assert(sizeof(PrepShared) <= 80 * 1024, "two prepare workgroups per CU");
 // goes to ring slot c % ring. Two workgroups per CU is what the LDS allows,
 // so the register budget is that of two waves per SIMD (256 per lane): the
 // compiler then keeps S3's MFMA results in VGPRs instead of AGPRs.
+// seg_w > 0 (the affine form of one sequence): the chunks are numbered in
+// segments of seg_w and every segment's first chunks are written last,
+// since the affine form's first pass scans all segments at once.
 template <int GATE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_prepare_kernel(
-    const KdaChunkArgs a, char *ws, int ring, int c_lo, int c_hi) {
+    const KdaChunkArgs a, char *ws, int ring, int c_lo, int c_hi, int seg_w) {
     __shared__ PrepShared sm;
     // Workgroups run chunk-descending, heads fastest: the scan starts with the
     // first chunk of every sequence and head, so those records are written
     // last and are still in the memory-side cache when it reads them (plain
     // write-back stores; with this order they beat nontemporal ones by 2%).
     const int H = a.num_heads;
-    const int c = (c_hi - 1) - static_cast<int>(blockIdx.x) / H;
+    int c = (c_hi - 1) - static_cast<int>(blockIdx.x) / H;
+    if (seg_w > 0) {
+        const int segs = (c_hi + seg_w - 1) / seg_w;
+        const int i = static_cast<int>(blockIdx.x) / H;
+        c = (i % segs) * seg_w + (seg_w - 1 - i / segs);
+        if (c >= c_hi) {
+            return;
+        }
+    }
     const int h = static_cast<int>(blockIdx.x) % H;
     const int N = a.num_seqs;
     const Layout LY = layout(a.num_tokens, N, H, ring);
@@ -748,7 +788,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int sl = 0; sl < 2; ++sl) {
             load_g8(16 * I + kAnchorRow, 2 * sh + sl, anc[sl]);
         }
-        bf16x8 Rh[2], Qh[2], Ql[2];
+        bf16x8 Rh[2], Rl[2], Qh[2], Ql[2];
         float qg[2][8];  // q e^G of this half's two slices: one record scale
         float ke[2][8];  // e^G k of the same rows and channels: one record scale
         float l1 = 0.f;  // this lane's share of the row's sum of |e^G k| over the half
@@ -769,7 +809,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 ke[sl][e] = kk[e] * eg;
                 l1 += fabsf(ke[sl][e]);
             }
-            Rh[sl] = to_bf16x8(rv);
+            split_bf16x8(rv, Rh[sl], Rl[sl]);
             split_bf16x8(qa, Qh[sl], Ql[sl]);
         }
         float *sc = reinterpret_cast<float *>(rec + kOffSc);
@@ -810,7 +850,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 }
                 bf16x8 Ch, Cl;
                 split_bf16x8(cv, Ch, Cl);
+                // Akk in three passes like Aqk: with one, its bf16 rounding
+                // (2^-9 per term) reaches T, and where the decay is weak the
+                // state keeps every chunk's error (8.5e-4 against 3.5e-4 of
+                // the final state's max after 16384 tokens at g ~ -1e-4)
                 akk = mfma(Rh[sl], Ch, akk);  // Akk[16I + 4gq + e][16J + r]
+                akk = mfma(Rh[sl], Cl, akk);
+                akk = mfma(Rl[sl], Ch, akk);
                 aqt = mfma(Ch, Qh[sl], aqt);  // Aqk[16I + r][16J + 4gq + e]
                 aqt = mfma(Ch, Ql[sl], aqt);
                 aqt = mfma(Cl, Qh[sl], aqt);
@@ -1301,17 +1347,30 @@ __device__ __forceinline__ void split_f16x2(float x0, float x1, int sh, uint32_t
 // goes to the carry area until the segment that holds the last chunk);
 // without it every launch scans whole sequences and the segment logic
 // compiles away. Chunk c's record is in ring slot c % ring.
-template <int NT, bool SEG>
+//
+// AFF: the first pass of the affine form of one sequence, s_lo = P
+// segments of s_hi = W chunks. The scan is linear in (initial state, v), so
+// a later segment s (chunks [sW, sW + W)) runs as two independent scans
+// from its start: from zero with the real v (outputs o', final state Z_s)
+// and from the identity with v = 0 (outputs O, final state Phi_s, the
+// segment's transition), while segment 0 runs as usual from the pool.
+// Every (role, head) is a chain of its own: role 0 is segment 0, roles
+// 2s - 1 and 2s the zero-start and identity-start scans of segment s. The
+// later roles write fp32 outputs and their final and tracked states to the
+// affine areas; chunk_affine_combine_kernel and chunk_affine_correct_kernel
+// finish the sequence.
+template <int NT, bool SEG, bool AFF = false>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws,
                                                                   int ring, int s_lo, int s_hi) {
     using St = Stage<NT>;
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
+    static_assert(!AFF || (NT == 1 && !SEG), "the affine pass scans 16-column groups of one sequence");
     __shared__ ScanShared<NT> sm;
 
     const int H = a.num_heads;
     const int N = a.num_seqs;
-    const int pairs = N * H;
+    const int pairs = AFF ? H * (2 * s_lo - 1) : N * H;
     // XCD-aware order: the NV column groups of one (sequence, head) share an
     // XCD (and its L2), since they read the same chunk records.
     const int b = blockIdx.x;
@@ -1322,8 +1381,13 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     if (pair >= pairs) {
         return;
     }
-    const int n = pair / H;
-    const int h = pair - n * H;
+    // AFF: the chain's role (0: segment 0; 2s - 1: zero start, 2s: identity
+    // start of segment s) in place of the sequence index (a single sequence)
+    const int role = AFF ? pair / H : 0;
+    const bool aff_zero = AFF && (role & 1) != 0;
+    const bool aff_phi = AFF && role > 0 && (role & 1) == 0;
+    const int n = AFF ? 0 : pair / H;
+    const int h = AFF ? pair - role * H : pair - n * H;
     const Layout LY = layout(a.num_tokens, N, H, ring);
     const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
     int bos, eos;
@@ -1346,6 +1410,34 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         j1 = s_hi < nch ? s_hi : nch;
         first = s_lo == 0;
         last = s_hi >= nch;
+    }
+    // AFF: the later roles start from zero or the identity and end in the
+    // affine areas (fin_state), tracking into them too (trk_state); their
+    // outputs are fp32 (out32); only role 0 writes the rows outside the
+    // sequence
+    float *fin_state = nullptr;
+    float *trk_state = nullptr;
+    float *out32 = nullptr;
+    bool zero_outside = false;
+    if constexpr (AFF) {
+        const int seg = (role + 1) >> 1;
+        j0 = seg * s_hi;
+        j1 = j0 + s_hi < nch ? j0 + s_hi : nch;
+        if (j0 >= nch && !(role == 0 && nch == 0)) {
+            return;
+        }
+        first = role == 0;
+        last = role == 0 && j1 >= nch;
+        zero_outside = role == 0;
+        if (role > 0) {
+            const AffLayout AL = aff_layout(a.num_tokens, H, s_lo);
+            char *wsm = const_cast<char *>(ws);
+            const size_t st = static_cast<size_t>(H) * DK * DK * 4;
+            const size_t hoff = static_cast<size_t>(h) * DK * DK;
+            fin_state = reinterpret_cast<float *>(wsm + (aff_zero ? AL.fin_zero : AL.fin_phi) + st * (seg - 1)) + hoff;
+            trk_state = reinterpret_cast<float *>(wsm + (aff_zero ? AL.trk_zero : AL.trk_phi)) + hoff;
+            out32 = reinterpret_cast<float *>(wsm + (aff_zero ? AL.out_zero : AL.out_phi));
+        }
     }
     float *carry = reinterpret_cast<float *>(const_cast<char *>(ws) + LY.carry) +
                    static_cast<size_t>(h) * DK * DK;
@@ -1402,7 +1494,13 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                if (!first) {
+                if (AFF && role > 0) {
+                    // zero, or the identity's columns col0 + 16ct + r
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        S[tt][ct][i] = aff_phi && 16 * (2 * wr + tt) + 4 * gq + i == col0 + 16 * ct + r ? 1.f : 0.f;
+                    }
+                } else if (!first) {
                     const float4 s4 = load4(carry_ptr(tt, ct));
                     S[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
                 } else if (slot > 0) {
@@ -1413,6 +1511,24 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         }
+        // the tracked state's element: the pool's track slot, or the affine
+        // area of a later role
+        auto track_ptr = [&](int tt, int ct) {
+            if (AFF && trk_state != nullptr) {
+                return trk_state + static_cast<int64_t>(col0 + 16 * ct + r) * DK + 16 * (2 * wr + tt) + 4 * gq;
+            }
+            return state_ptr(track_slot, tt, ct);
+        };
+        auto store_track = [&](const f32x4 (&val)[2][NT]) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    *reinterpret_cast<float4 *>(track_ptr(tt, ct)) =
+                        make_float4(val[tt][ct][0], val[tt][ct][1], val[tt][ct][2], val[tt][ct][3]);
+                }
+            }
+        };
         auto store_S = [&](int dst_slot, const f32x4 (&val)[2][NT]) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
@@ -1591,7 +1707,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                             tu = mfma(th, vl[s], tu);
                         }
                         const float f = tsc[2 * wr + tt] * inv_v;
-                        *reinterpret_cast<float4 *>(state_ptr(track_slot, tt, ct)) =
+                        *reinterpret_cast<float4 *>(track_ptr(tt, ct)) =
                             make_float4(S[tt][ct][0] * g2[0] + tu[0] * f, S[tt][ct][1] * g2[1] + tu[1] * f,
                                         S[tt][ct][2] * g2[2] + tu[2] * f, S[tt][ct][3] * g2[3] + tu[3] * f);
                     }
@@ -1612,7 +1728,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
             if (track_slot > 0 && rr == len) {
-                store_S(track_slot, S);
+                store_track(S);
             }
         };
 
@@ -1623,7 +1739,17 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         if (j1 > j0) {
             lds_barrier();  // B1(j1)
         }
-        if (!last) {
+        if (AFF && fin_state != nullptr) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    *reinterpret_cast<float4 *>(fin_state + static_cast<int64_t>(col0 + 16 * ct + r) * DK +
+                                                16 * (2 * wr + tt) + 4 * gq) =
+                        make_float4(S[tt][ct][0], S[tt][ct][1], S[tt][ct][2], S[tt][ct][3]);
+                }
+            }
+        } else if (!last) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
@@ -1674,6 +1800,24 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // this wave's LDS tile so each lane writes CW/4 consecutive columns of
         // one row (nontemporal stores).
         auto finish = [&](int j) {
+            if (AFF && out32 != nullptr) {
+                // a later affine role: fp32 rows, straight from the C tiles
+                // (16 lanes write 64 consecutive bytes of one row)
+                const int t0 = bos + BT * j;
+                const int len = eos - t0 < BT ? eos - t0 : BT;
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    const f32x4 acc = P[ct] + A[ct];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = 16 * wr + 4 * gq + i;
+                        if (t < len) {
+                            out32[(static_cast<int64_t>(t0 + t) * H + h) * DK + col0 + 16 * ct + r] = acc[i];
+                        }
+                    }
+                }
+                return;
+            }
             uint16_t *ot = reinterpret_cast<uint16_t *>(&sm.otile[wr][0][0]);
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
@@ -1818,6 +1962,13 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
         };
         auto fetch_v = [&](uint2 (&V)[NT], int j) {
+            if (aff_phi) {  // the identity-start scan runs on v = 0
+#pragma unroll
+                for (int k = 0; k < NT; ++k) {
+                    V[k] = make_uint2(0u, 0u);
+                }
+                return;
+            }
             const int jc = j < j1 ? j : j1 - 1;
             const int t0 = bos + BT * jc;
             const int len = eos - t0 < BT ? eos - t0 : BT;
@@ -1945,8 +2096,280 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     if (n == 0 && first) {
         zero_rows(0, bos);
     }
-    if (n == N - 1 && last) {
+    if (n == N - 1 && (last || zero_outside)) {
         zero_rows(eos, a.num_tokens);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The affine form of one long sequence on few heads: chunk_scan_kernel<1,
+// false, true> scans segment 0 from the pool and every later segment s
+// twice from its start (from zero with the real v: outputs o', final state
+// Z_s; from the identity with v = 0: outputs O, final state Phi_s). With
+// S_s the true state at segment s's start,
+//     S_{s+1} = Phi_s S_s + Z_s,     o_t = o'_t + O_t S_s   (t in segment s),
+// since the recurrence and the readout are linear in (state, v). The first
+// is a short serial pass over the segments (this kernel); the second a
+// parallel product over the later segments' chunks (the next one). The
+// chains of the first pass fill the CUs a few-head sequence leaves idle.
+// ---------------------------------------------------------------------------
+
+constexpr int kAffThreads = 256;
+
+// One workgroup per (head, 16 value columns): S_s for s = 1 .. P-1 (the true
+// state at each later segment's start, kept for the correction), the
+// tracked state when the tracked length ends inside a later segment (its
+// two tracked scan states combined the same way), and the final state into
+// the pool. Each 128 x 128 transition is staged in LDS with wide loads, then
+// multiplied in fp32, element k of a column summed over v' in order.
+__global__ __launch_bounds__(kAffThreads) void chunk_affine_combine_kernel(const KdaChunkArgs a, char *ws,
+                                                                         int P, int W) {
+    __shared__ float mat[DK][DK];     // the staged transition, [v'][k] as stored
+    __shared__ float4 cur[2][DK][4];  // S_s columns: [buffer][v' = K index][16 columns as 4 float4]
+    const int H = a.num_heads;
+    const int h = blockIdx.x >> 3;
+    const int g = blockIdx.x & 7;
+    if (h >= H) {
+        return;
+    }
+    int bos, eos;
+    seq_bounds(a, 0, bos, eos);
+    const int nch = (eos - bos + BT - 1) / BT;
+    if (nch <= W) {
+        return;  // segment 0 held the whole sequence and finished it
+    }
+    int slot = a.state_indices[0];
+    if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
+        slot = 0;
+    }
+    int track_slot = 0;
+    int track_len = -1;
+    if (a.track_indices != nullptr) {
+        track_slot = a.track_indices[0];
+        if (track_slot <= 0 || static_cast<int64_t>(track_slot) >= a.num_slots) {
+            track_slot = 0;
+        } else {
+            track_len = a.track_lens[0];
+        }
+    }
+    const Layout LY = layout(a.num_tokens, 1, H);
+    const AffLayout AL = aff_layout(a.num_tokens, H, P);
+    const size_t st = static_cast<size_t>(H) * DK * DK * 4;
+    const size_t hoff = static_cast<size_t>(h) * DK * DK;
+    auto area = [&](size_t off, int s) { return reinterpret_cast<float *>(ws + off + st * s) + hoff; };
+    const int tid = threadIdx.x;
+    const int k = tid & (DK - 1);  // this thread's K row
+    const int vh = tid >> 7;       // its 8 columns: 16 g + 8 vh + e
+    const int col = 16 * g + 8 * vh;
+    // S_1 = segment 0's final state (the carry area, [V][K])
+    const float *carry = reinterpret_cast<const float *>(ws + LY.carry) + hoff;
+    for (int e = 0; e < 8; ++e) {
+        reinterpret_cast<float *>(&cur[0][k][2 * vh])[e] = carry[static_cast<int64_t>(col + e) * DK + k];
+    }
+    // The transitions stream through `mat` (64 KiB, 16 float4 per thread):
+    // Phi_{s+1} and Z_{s+1} are loaded into registers while step s multiplies.
+    float4 rg[16];
+    float zz[8];
+    auto fetch = [&](const float *M, const float *Z) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            rg[i] = reinterpret_cast<const float4 *>(M)[tid + kAffThreads * i];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            zz[e] = Z[static_cast<int64_t>(col + e) * DK + k];
+        }
+    };
+    auto put = [&]() {
+        __syncthreads();  // every reader of the previous matrix is done
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            reinterpret_cast<float4 *>(&mat[0][0])[tid + kAffThreads * i] = rg[i];
+        }
+        __syncthreads();
+    };
+    // acc[e] += sum_v' mat[v'][k] cur[v'][col + e]
+    auto product = [&](int b, float (&acc)[8]) {
+#pragma unroll 8
+        for (int v2 = 0; v2 < DK; ++v2) {
+            const float m = mat[v2][k];
+            const float4 c0 = cur[b][v2][2 * vh];
+            const float4 c1 = cur[b][v2][2 * vh + 1];
+            acc[0] = fmaf(m, c0.x, acc[0]);
+            acc[1] = fmaf(m, c0.y, acc[1]);
+            acc[2] = fmaf(m, c0.z, acc[2]);
+            acc[3] = fmaf(m, c0.w, acc[3]);
+            acc[4] = fmaf(m, c1.x, acc[4]);
+            acc[5] = fmaf(m, c1.y, acc[5]);
+            acc[6] = fmaf(m, c1.z, acc[6]);
+            acc[7] = fmaf(m, c1.w, acc[7]);
+        }
+    };
+    const int64_t head_off = static_cast<int64_t>(h) * a.state_stride_head;
+    auto pool_col = [&](int s_, int e) {
+        return a.state + s_ * a.state_stride_slot + head_off + static_cast<int64_t>(col + e) * DK + k;
+    };
+    int b = 0;
+    fetch(area(AL.fin_phi, 0), area(AL.fin_zero, 0));
+    for (int s = 1; s < P && s * W < nch; ++s) {
+        // S_s, kept for the correction of segment s's outputs
+        float *start = area(AL.start, s - 1);
+        for (int e = 0; e < 8; ++e) {
+            start[static_cast<int64_t>(col + e) * DK + k] = reinterpret_cast<const float *>(&cur[b][k][2 * vh])[e];
+        }
+        // a tracked length inside segment s: tokens (64 s W, min(64 (s+1) W, len)]
+        // (at most one segment holds it: its two tracked states pass through
+        // `mat` first, Phi_s's loads waiting in registers)
+        const int seg_end = (s + 1) * W < nch ? BT * (s + 1) * W : eos - bos;
+        if (track_slot > 0 && track_len > BT * s * W && track_len <= seg_end) {
+            const float *tphi = reinterpret_cast<const float *>(ws + AL.trk_phi) + hoff;
+            const float *tz = reinterpret_cast<const float *>(ws + AL.trk_zero) + hoff;
+            float4 tr[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                tr[i] = reinterpret_cast<const float4 *>(tphi)[tid + kAffThreads * i];
+            }
+            float acc[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                acc[e] = tz[static_cast<int64_t>(col + e) * DK + k];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                reinterpret_cast<float4 *>(&mat[0][0])[tid + kAffThreads * i] = tr[i];
+            }
+            __syncthreads();
+            product(b, acc);
+            for (int e = 0; e < 8; ++e) {
+                *pool_col(track_slot, e) = acc[e];
+            }
+        }
+        put();  // Phi_s into mat
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            acc[e] = zz[e];
+        }
+        if (s + 1 < P && (s + 1) * W < nch) {
+            fetch(area(AL.fin_phi, s), area(AL.fin_zero, s));
+        }
+        product(b, acc);
+        for (int e = 0; e < 8; ++e) {
+            reinterpret_cast<float *>(&cur[b ^ 1][k][2 * vh])[e] = acc[e];
+        }
+        b ^= 1;  // the next put's first barrier orders these writes before any read
+    }
+    if (slot > 0) {
+        for (int e = 0; e < 8; ++e) {
+            *pool_col(slot, e) = reinterpret_cast<const float *>(&cur[b][k][2 * vh])[e];
+        }
+    }
+}
+
+// Chunks per correction workgroup (they share the staged S_s).
+constexpr int kAffCorrectChunks = 4;
+
+// One workgroup per (later segment s, head, kAffCorrectChunks of the
+// segment's chunks): o_t = bf16(o'_t + O_t S_s). S_s is staged once as bf16
+// hi + lo B fragments (64 KiB), each 16-row tile of O is split likewise, and
+// the product takes three passes (hi hi, hi lo, lo hi: about 2^-16 relative
+// per term). Wave w takes token rows [16w, 16w + 16) of each chunk.
+__global__ __launch_bounds__(kAffThreads) void chunk_affine_correct_kernel(const KdaChunkArgs a, char *ws, int P,
+                                                                         int W) {
+    __shared__ u32x4 sb[4][8][2][64];  // S_s B fragments: [K slice][column tile][hi, lo][lane]
+    const int H = a.num_heads;
+    const int groups = (W + kAffCorrectChunks - 1) / kAffCorrectChunks;
+    const int s = 1 + static_cast<int>(blockIdx.x) / (groups * H);
+    const int rest = static_cast<int>(blockIdx.x) % (groups * H);
+    const int h = rest % H;
+    const int c_lo = s * W + (rest / H) * kAffCorrectChunks;
+    int bos, eos;
+    seq_bounds(a, 0, bos, eos);
+    const int nch = (eos - bos + BT - 1) / BT;
+    const int seg_hi = (s + 1) * W < nch ? (s + 1) * W : nch;
+    if (s >= P || c_lo >= seg_hi) {
+        return;
+    }
+    const int c_hi = c_lo + kAffCorrectChunks < seg_hi ? c_lo + kAffCorrectChunks : seg_hi;
+    const AffLayout AL = aff_layout(a.num_tokens, H, P);
+    const float *S = reinterpret_cast<const float *>(ws + AL.start + static_cast<size_t>(H) * DK * DK * 4 * (s - 1)) +
+                     static_cast<size_t>(h) * DK * DK;
+    const float *O = reinterpret_cast<const float *>(ws + AL.out_phi);
+    const float *Oz = reinterpret_cast<const float *>(ws + AL.out_zero);
+    uint16_t *out = static_cast<uint16_t *>(a.out);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane & 15;
+    const int gq = lane >> 4;
+    // S_s as B fragments: lane (r, gq) of fragment (slice sl, tile nt) holds
+    // S[k = 32 sl + kperm(gq, e)][v = 16 nt + r]; S is [V][K], so each half
+    // of the eight is one float4 run of K
+    for (int f = w; f < 32; f += 4) {
+        const int sl = f & 3;
+        const int nt = f >> 2;
+        const float *col = S + static_cast<int64_t>(16 * nt + r) * DK + 32 * sl + 4 * gq;
+        const float4 x0 = *reinterpret_cast<const float4 *>(col);
+        const float4 x1 = *reinterpret_cast<const float4 *>(col + 16);
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        bf16x8 hi, lo;
+        split_bf16x8(x, hi, lo);
+        sb[sl][nt][0][lane] = as_u32x4(hi);
+        sb[sl][nt][1][lane] = as_u32x4(lo);
+    }
+    __syncthreads();
+    for (int c = c_lo; c < c_hi; ++c) {
+        const int t0 = bos + BT * c;
+        const int len = eos - t0 < BT ? eos - t0 : BT;
+        // A: row 16 w + r of O (rows past the chunk's end read its last row;
+        // their results are not stored)
+        const int ta = 16 * w + r < len ? 16 * w + r : len - 1;
+        const float *orow = O + (static_cast<int64_t>(t0 + ta) * H + h) * DK;
+        float4 ox[4][2];
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            ox[sl][0] = *reinterpret_cast<const float4 *>(orow + 32 * sl + 4 * gq);
+            ox[sl][1] = *reinterpret_cast<const float4 *>(orow + 32 * sl + 16 + 4 * gq);
+        }
+        // o' of this lane's outputs, loaded before the products need them
+        // (rows past the chunk's end read its last row)
+        float oz[8][4];
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * w + 4 * gq + i < len ? 16 * w + 4 * gq + i : len - 1;
+                oz[nt][i] = Oz[(static_cast<int64_t>(t0 + t) * H + h) * DK + 16 * nt + r];
+            }
+        }
+        bf16x8 ah[4], al[4];
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            const float x[8] = {ox[sl][0].x, ox[sl][0].y, ox[sl][0].z, ox[sl][0].w,
+                                ox[sl][1].x, ox[sl][1].y, ox[sl][1].z, ox[sl][1].w};
+            split_bf16x8(x, ah[sl], al[sl]);
+        }
+#pragma unroll 2
+        for (int nt = 0; nt < 8; ++nt) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                const bf16x8 bh = as_bf16x8(sb[sl][nt][0][lane]);
+                const bf16x8 bl = as_bf16x8(sb[sl][nt][1][lane]);
+                acc = mfma(ah[sl], bh, acc);
+                acc = mfma(ah[sl], bl, acc);
+                acc = mfma(al[sl], bh, acc);
+            }
+            // lane (r, gq) holds C[4 gq + i][r]: token 16 w + 4 gq + i, column 16 nt + r
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * w + 4 * gq + i;
+                if (t < len) {
+                    out[(static_cast<int64_t>(t0 + t) * H + h) * DK + 16 * nt + r] = f32_to_bf16(oz[nt][i] + acc[i]);
+                }
+            }
+        }
     }
 }
 
@@ -1981,6 +2404,8 @@ int device_cus(hipStream_t stream) {
 // once (pairs x 8 <= CUs), the wide ones as soon as the narrow ones would need
 // a second round.
 int scan_tiles(int64_t pairs, hipStream_t stream) { return pairs * 8 <= device_cus(stream) ? 1 : 2; }
+
+const void *scan_kernel_affine() { return reinterpret_cast<const void *>(chunk_scan_kernel<1, false, true>); }
 
 const void *scan_kernel(int nt, bool seg) {
     if (nt == 2) {
@@ -2093,10 +2518,48 @@ int window_chunks(int T) {
     return segs == 2 ? nch - first : first;
 }
 
-// The workspace a call needs: the ring of 2W slots for the segmented shape,
-// one slot per chunk otherwise.
-size_t required_bytes(int T, int N, int H) {
+// The affine form of a single sequence (see chunk_affine_combine_kernel):
+// its first pass runs 8 (2P - 1) H scan workgroups, each on a CU of its own,
+// so it applies while at least two segments fit the device, with segments of
+// at least kAffMinChunks chunks (the combine's serial steps and the extra
+// launches cost a few microseconds each). Returns P (0: not applicable) and
+// the segment length W in chunks.
+// Its workspace keeps every record and two fp32 outputs per token, so it is
+// taken only while that stays within kAffMaxBytes (at 4 heads about 130,000
+// tokens); longer sequences keep the pipelined segments.
+// With two segments it does not pay (measured: 8 heads x 16384 tokens 321
+// against 312 us, 4 x 4096 96 against 80 us): the first pass's chains run
+// slower than the one-pass scan's, so it needs at least three.
+constexpr int kAffMinChunks = 32;
+constexpr int kAffMinSegments = 3;
+constexpr size_t kAffMaxBytes = size_t{1} << 30;
+
+int affine_segments(int T, int H, int cus, int &W) {
+    const int nch = chunk_bound(T);
+    int P = 0;
+    for (int p = 2; 8 * H * (2 * p - 1) <= cus; ++p) {
+        if ((nch + p - 1) / p < kAffMinChunks) {
+            break;
+        }
+        P = p;
+    }
+    if (P < kAffMinSegments || aff_layout(T, H, P).total > kAffMaxBytes) {
+        P = 0;
+    }
+    W = P > 0 ? (nch + P - 1) / P : 0;
+    return P;
+}
+
+// The workspace a call needs: the affine form's areas for a single sequence
+// that takes it, the ring of 2W slots for the segmented shape, one slot per
+// chunk otherwise.
+size_t classic_bytes(int T, int N, int H) {
     return windowed_shape(T, N, H) ? layout(T, 1, H, 2 * window_chunks(T)).total : layout(T, N, H).total;
+}
+size_t required_bytes(int T, int N, int H, int cus) {
+    int W = 0;
+    const int P = N == 1 ? affine_segments(T, H, cus, W) : 0;
+    return P > 0 ? aff_layout(T, H, P).total : classic_bytes(T, N, H);
 }
 
 // The largest window (segments run one after another, so a ring of W slots)
@@ -2120,7 +2583,7 @@ extern "C" size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs
     if (num_tokens < 0 || num_seqs < 0 || num_heads <= 0 || head_dim != kda::chunk::DK) {
         return 0;
     }
-    return kda::chunk::required_bytes(num_tokens, num_seqs, num_heads);
+    return kda::chunk::required_bytes(num_tokens, num_seqs, num_heads, kda::chunk::device_cus(nullptr));
 }
 
 namespace kda {
@@ -2199,8 +2662,8 @@ int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, int ring, int win, b
         if (hi <= lo) {
             return true;
         }
-        int rg = ring, l = lo, h = hi;
-        void *params[] = {&kargs, &ws, &rg, &l, &h};
+        int rg = ring, l = lo, h = hi, sw = 0;
+        void *params[] = {&kargs, &ws, &rg, &l, &h, &sw};
         return hipLaunchKernel(prep, dim3(static_cast<unsigned>(static_cast<int64_t>(hi - lo) * a.num_heads)),
                                dim3(kThreads), params, 0, s) == hipSuccess;
     };
@@ -2266,6 +2729,50 @@ int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, int ring, int win, b
     return KDA_OK;
 }
 
+// The affine form of one sequence, all on `st`: K1 over every chunk, the
+// first pass (segment 0 from the pool, the later segments from zero and from
+// the identity), the serial combine, the parallel correction of the later
+// segments' outputs.
+int launch_affine(const KdaChunkArgs &a, char *ws, hipStream_t st, int P, int W) {
+    KdaChunkArgs kargs = a;
+    const int H = a.num_heads;
+    const int nrec = max_chunks(a.num_tokens, 1);
+    const int nch_max = chunk_bound(a.num_tokens);
+    const int64_t blocks = scan_blocks(static_cast<int64_t>(H) * (2 * P - 1), 1);
+    if (static_cast<int64_t>(nrec) * H > 0x7fffffff || blocks > 0x7fffffff) {
+        return KDA_ERR_INVALID_ARGUMENT;
+    }
+    const void *prep = a.gate_mode == KDA_GATE_RAW
+                           ? reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_RAW>)
+                           : reinterpret_cast<const void *>(chunk_prepare_kernel<KDA_GATE_LOG>);
+    // every chunk, numbered in segments of W chunks (P W >= nrec - 1 >= the chunks)
+    int ring = nrec, lo = 0, hi = nch_max, order = W;
+    void *pparams[] = {&kargs, &ws, &ring, &lo, &hi, &order};
+    if (hipLaunchKernel(prep, dim3(static_cast<unsigned>(static_cast<int64_t>(P) * W * H)), dim3(kThreads), pparams,
+                        0, st) != hipSuccess) {
+        return KDA_ERR_LAUNCH;
+    }
+    const char *cws = ws;
+    int sp = P, sw = W;
+    void *sparams[] = {&kargs, &cws, &ring, &sp, &sw};
+    if (hipLaunchKernel(scan_kernel_affine(), dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads), sparams, 0,
+                        st) != hipSuccess) {
+        return KDA_ERR_LAUNCH;
+    }
+    void *cparams[] = {&kargs, &ws, &sp, &sw};
+    if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_affine_combine_kernel), dim3(static_cast<unsigned>(8 * H)),
+                        dim3(kAffThreads), cparams, 0, st) != hipSuccess) {
+        return KDA_ERR_LAUNCH;
+    }
+    const int64_t later = static_cast<int64_t>(P - 1) * ((W + kAffCorrectChunks - 1) / kAffCorrectChunks) * H;
+    if (nch_max > W && later > 0 &&
+        hipLaunchKernel(reinterpret_cast<const void *>(chunk_affine_correct_kernel), dim3(static_cast<unsigned>(later)),
+                        dim3(kAffThreads), cparams, 0, st) != hipSuccess) {
+        return KDA_ERR_LAUNCH;
+    }
+    return KDA_OK;
+}
+
 // The no-allocation entry point's scratch: one array per device, held until
 // the process ends. Host code never uses the array's name as an address: the
 // device address is resolved once per device with hipGetSymbolAddress (that
@@ -2323,7 +2830,14 @@ extern "C" int kda_chunk_launch(const KdaChunkArgs *args, void *workspace, size_
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int T = a.num_tokens;
     const int H = a.num_heads;
-    if (workspace_bytes >= required_bytes(T, a.num_seqs, H)) {
+    if (a.num_seqs == 1) {
+        int W = 0;
+        const int P = affine_segments(T, H, device_cus(st), W);
+        if (P > 0 && workspace_bytes >= aff_layout(T, H, P).total) {
+            return launch_affine(a, ws, st, P, W);
+        }
+    }
+    if (workspace_bytes >= classic_bytes(T, a.num_seqs, H)) {
         if (windowed_shape(T, a.num_seqs, H)) {
             const int w = window_chunks(T);
             return launch(a, ws, st, 2 * w, w, true, first_segment(T));

@@ -178,11 +178,16 @@ typedef struct KdaChunkArgs {
 } KdaChunkArgs;
 
 /* Bytes of device scratch kda_chunk_launch needs to run these arguments at
- * full speed. An upper bound that depends only on T, N, H and D (no device
- * reads): the chunk records (one per possible chunk and head, or, for a
- * single sequence of at least 16384 tokens on at most 16 heads, a ring of two
- * scan segments' records per head), the tracking records and, when N == 1,
- * the state carried between scan segments. */
+ * full speed. An upper bound that depends only on T, N, H, D and the current
+ * device's compute-unit count (no device reads): the chunk records (one per
+ * possible chunk and head, or, for a single sequence of at least 16384 tokens
+ * on at most 16 heads, a ring of two scan segments' records per head), the
+ * tracking records and, when N == 1, the state carried between scan
+ * segments. A single sequence that takes the affine form (at most 6 heads on
+ * 256 CUs, at least 3 segments of 32 chunks, at most 1 GiB in all) needs one
+ * record per chunk, two fp32 outputs per token-head and 3 (P - 1) + 2 sets of
+ * H fp32 128 x 128 states besides; with less than that but at least the other forms'
+ * size, kda_chunk_launch runs those. */
 size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
                                  int32_t num_heads, int32_t head_dim);
 
@@ -203,7 +208,11 @@ size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
  * With the full workspace, a single sequence of at least 16384 tokens on at
  * most 16 heads runs in segments of about 256 chunks: each next segment is
  * prepared on a library-owned stream while the current one is scanned, forked
- * from and joined back on `stream` by events (graph-capture safe).
+ * from and joined back on `stream` by events (graph-capture safe); a single
+ * sequence on few heads that takes the affine form scans its P segments at
+ * once (segment s > 0 from zero and from the identity) and combines them
+ * (S_{s+1} = Phi_s S_s + Z_s, outputs corrected by O_t S_s), all on
+ * `stream`.
  * Alignment
  * (KDA_ERR_INVALID_ARGUMENT otherwise): state 16 bytes with strides in
  * multiples of 4 elements; q, k, v and out 8 bytes; gate 8 (RAW) or 16. */

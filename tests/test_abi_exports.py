@@ -153,13 +153,22 @@ def test_chunk_workspace_size_formula(lib):
     per possible (chunk, head), except for a single sequence of at least 16384
     tokens on at most 16 heads, which runs in S = max(2, ceil(chunks / 256))
     segments (two: 47% and 53% of the chunks; more: W = ceil(chunks / S)
-    each) and needs a ring of two of the longest per head."""
+    each) and needs a ring of two of the longest per head.
+
+    A single sequence whose scan leaves most of a 256-CU device idle takes
+    the affine form instead: P segments, the most for which its first pass's
+    8 (2P - 1) H workgroups fit the CUs with segments of at least 32 chunks,
+    when that is at least three and the total stays within 1 GiB. It keeps one record per chunk and
+    adds two fp32 outputs per token-head, and five sets of H 64 KiB states
+    ((P - 1) each for the two scans' final states and the segment starts,
+    one each for the two scans' tracked states)."""
     lib.kda_chunk_workspace_bytes.restype = ctypes.c_size_t
     lib.kda_chunk_workspace_bytes.argtypes = [ctypes.c_int32] * 4
     rec, track = 56320, 17152
     assert rec == 55 * 1024 and track == 16.75 * 1024
-    for T, N, H in [(8192, 1, 32), (33814, 16, 32), (65536, 1, 16), (65536, 1, 17), (16383, 1, 4),
-                    (16384, 1, 4), (100000, 1, 8), (1, 1, 1), (0, 3, 2)]:
+    cus = 256  # no device here: the library assumes MI355X's count
+
+    def classic(T, N, H):
         header = ((N + 1) * 4 + 255) // 256 * 256
         chunks = (T + 63) // 64
         slots = chunks + N
@@ -167,8 +176,32 @@ def test_chunk_workspace_size_formula(lib):
             segs = max(2, (chunks + 255) // 256)
             first = (chunks * 47 + 50) // 100 if segs == 2 else (chunks + segs - 1) // segs
             slots = 2 * (chunks - first if segs == 2 else first)
-        expected = header + rec * slots * H + track * N * H + (65536 * H if N == 1 else 0)
+        return header + rec * slots * H + track * N * H + (65536 * H if N == 1 else 0)
+
+    def affine(T, H):
+        chunks = (T + 63) // 64
+        P = 0
+        p = 2
+        while 8 * H * (2 * p - 1) <= cus and (chunks + p - 1) // p >= 32:
+            P = p
+            p += 1
+        if P < 3:
+            return None
+        outs = 2 * ((T * H * 512 + 255) // 256 * 256)
+        one_pass = 256 + rec * (chunks + 1) * H + track * H + 65536 * H
+        total = one_pass + outs + 65536 * H * (3 * (P - 1) + 2)
+        return total if total <= 1 << 30 else None
+
+    for T, N, H in [(8192, 1, 32), (33814, 16, 32), (65536, 1, 16), (65536, 1, 17), (16383, 1, 4),
+                    (16384, 1, 4), (100000, 1, 8), (1, 1, 1), (0, 3, 2), (4096, 1, 8), (4095, 1, 8),
+                    (16384, 1, 1), (400000, 1, 4), (6144, 1, 4), (5952, 1, 4), (6144, 1, 6), (6144, 1, 7)]:
+        expected = (affine(T, H) if N == 1 else None) or classic(T, N, H)
         assert lib.kda_chunk_workspace_bytes(T, N, H, 128) == expected, (T, N, H)
+    # which shapes take the affine form
+    assert affine(16384, 4) and affine(6144, 4) and affine(16384, 1) and affine(6144, 6)
+    assert not affine(65536, 16) and not affine(8192, 32) and not affine(16384, 8)
+    assert not affine(4096, 4) and not affine(6144, 7) and not affine(5952, 4)
+    assert not affine(400000, 4) and not affine(100000, 8)  # beyond 1 GiB
 
 
 def test_noalloc_rejects_what_its_scratch_cannot_hold(lib):

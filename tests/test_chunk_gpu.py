@@ -222,6 +222,26 @@ def test_prepared_chunk_strong_decay(gpu_ops, label, gfun):
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, f"{label} pool")
 
 
+@pytest.mark.parametrize("heads,T", [(4, 4096), (2, 8192)])
+def test_prepared_chunk_weak_decay(gpu_ops, heads, T):
+    """Weak decay, g = logsigmoid(randn + 9) ~ -1.2e-4 per token: the state
+    remembers the whole sequence, so every chunk's rounding (in T, the record
+    operands and the published states) reaches the final state. Against the
+    fp64 oracle at the tolerance contract."""
+    case = C.prepared_case(heads, (T,), slots=3, indices=[1], seed=47, gate_shift=9.0)
+    dev = _prepared_dev(case)
+    pool = C.to_dev(case.pool, DEV)
+    out = _chunk_prepared(gpu_ops, case, pool, dev)
+    ref_pool = C.clone_pool(case.pool).double()
+    ref = R.kda_chunk(case.q.double() * case.scale, case.k.double(), case.v.double(),
+                      case.g.double(), case.beta.double(), state_pool=ref_pool,
+                      state_indices=case.indices, cu_seqlens=case.cu_seqlens,
+                      dtype=torch.float64, out_dtype=torch.float64)
+    e_o = C.assert_out(out.cpu(), ref, C.OUT_TOL, "weak decay output")
+    e_s = C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "weak decay pool")
+    print(f"weak decay H{heads} T{T}: output err {e_o:.2e}, state err {e_s:.2e}")
+
+
 def test_prepared_chunk_beyond_envelope_stays_finite(gpu_ops):
     """Per-token decays beyond the stated envelope (8 tokens at g = -20 span
     160 nat) give finite outputs and states: the factor exponents are clamped
@@ -273,6 +293,9 @@ def test_prepared_chunk_many_sequences(gpu_ops):
         ("config4", 32, None, 64, None, (1.0, 0.0)),
         # config 5 (prefill half): T=65536, H=16, harsh decay
         ("config5", 16, (65536,), 2, [1], (2.0, -2.0)),
+        # config 3's shape with weak decay, g = logsigmoid(randn + 9) ~ -1e-4:
+        # the state keeps every chunk's rounding for the whole sequence
+        ("config3 weak decay", 32, (8192,), 2, [1], (1.0, 9.0)),
     ],
 )
 def test_baseline_configs_chunk_vs_recurrent(gpu_ops, name, heads, lengths, slots, indices, gate):
@@ -282,7 +305,7 @@ def test_baseline_configs_chunk_vs_recurrent(gpu_ops, name, heads, lengths, slot
         indices = torch.randperm(64, generator=g_)[:16].tolist()
     case = C.prepared_case(heads, lengths, slots=slots, indices=indices, seed=len(name) + 3,
                            gate_scale=gate[0], gate_shift=gate[1],
-                           zero_pool=(name != "config4"))
+                           zero_pool=not name.startswith("config4"))
     dev = _prepared_dev(case)
     pool_c = C.to_dev(case.pool, DEV)
     pool_r = C.to_dev(case.pool, DEV)

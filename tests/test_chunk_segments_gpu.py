@@ -29,6 +29,15 @@ def _rec_bytes(lib):
     return lib.kda_chunk_workspace_bytes(128, 2, 1, 128) - lib.kda_chunk_workspace_bytes(64, 2, 1, 128)
 
 
+def _base_bytes(H):
+    """A single sequence's workspace without its records: the chunk-start
+    table, one tracking record and one carried state per head (the sizes
+    test_abi_exports pins). A workspace of this plus W records per head runs
+    windows of W chunks; with every chunk's record it runs in one pass (the
+    affine form, when the shape takes it, needs more than either)."""
+    return 256 + 17152 * H + 65536 * H
+
+
 def _launch(lib, case, nbytes, track=None):
     a, out, pool, keep = _prepare(case)
     if track is not None:
@@ -64,8 +73,9 @@ def test_small_workspace_runs_segments(label, lens, bounds, window, track):
         case = dataclasses.replace(case, cu_seqlens=torch.tensor(bounds, dtype=torch.int32))
     T, H, D = case.q.shape[1:]
     REC = _rec_bytes(lib)
-    full = lib.kda_chunk_workspace_bytes(T, 1, H, D)
-    base = full - REC * ((T + 63) // 64 + 1) * H
+    base = _base_bytes(H)
+    full = base + REC * ((T + 63) // 64 + 1) * H  # the one-pass form
+    assert full <= lib.kda_chunk_workspace_bytes(T, 1, H, D)
     small = base + REC * window * H
     assert small < full
     rc_ref, out_ref, pool_ref = _launch(lib, case, full, track)
@@ -79,15 +89,18 @@ def test_small_workspace_runs_segments(label, lens, bounds, window, track):
 
 
 def test_pipelined_segments_match_sequential_segments():
-    """A 16384-token sequence on 4 heads takes the pipelined segments with the
-    recommended workspace; the same call with a workspace for 13-chunk
-    segments run one after another gives the same bits."""
+    """A 16384-token sequence on 4 heads takes the pipelined segments with a
+    workspace of their ring (two segments, 120 and 136 chunks; less than the
+    affine form's, which kda_chunk_workspace_bytes recommends for this
+    shape); the same call with a workspace for 13-chunk segments run one
+    after another gives the same bits."""
     lib = _lib()
     case = C.prepared_case(4, (16384,), slots=3, indices=[1], seed=95)
     T, H, D = case.q.shape[1:]
     REC = _rec_bytes(lib)
-    ring = lib.kda_chunk_workspace_bytes(T, 1, H, D)
-    base = ring - REC * 2 * 136 * H  # two segments, 120 and 136 chunks
+    base = _base_bytes(H)
+    ring = base + REC * 2 * 136 * H
+    assert ring < lib.kda_chunk_workspace_bytes(T, 1, H, D)
     rc_a, out_a, pool_a = _launch(lib, case, ring, (2, 9000))
     rc_b, out_b, pool_b = _launch(lib, case, base + REC * 13 * H, (2, 9000))
     assert rc_a == 0 and rc_b == 0

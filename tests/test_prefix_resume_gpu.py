@@ -15,8 +15,8 @@ Here the same three checks run for both operators: ``kda_varlen_recurrent``
 (``prefill=True``: the token loop for short requests, the chunked kernels from
 128 tokens per request) and ``kda_varlen_chunk``, including a checkpoint
 inside a ragged last chunk and a single long sequence on few heads, which
-runs as pipelined scan segments (the tracked prefix then ends in the second
-segment). Suffix outputs and final states are checked against the fp32 oracle
+runs in the affine form (segments scanned in parallel and combined) or as
+pipelined scan segments (the tracked prefix then ends in a later segment). Suffix outputs and final states are checked against the fp32 oracle
 of the full run at the tolerance contract, and final states also against the
 full GPU run.
 """
@@ -63,28 +63,34 @@ def _oracle(case, pool_cpu):
                            out_dtype=torch.float32)
 
 
-# (label, heads, lengths, cuts, source slots, destination slots)
+# (label, heads, lengths, cuts, source slots, destination slots, raw lower bound)
 CASES = [
     # the reference's own layout: three short requests, one of them untracked
-    ("short varlen", 4, (100, 37, 63), (50, 37, 0), (3, 1, 5), (9, 7, 0)),
+    ("short varlen", 4, (100, 37, 63), (50, 37, 0), (3, 1, 5), (9, 7, 0), -5.0),
     # cuts inside ragged last chunks, one request on the padding slot 0;
     # 400 tokens over 2 requests take the chunked route in the recurrent op
-    ("ragged tails", 4, (300, 100), (290, 64), (2, 0), (6, 8)),
+    ("ragged tails", 4, (300, 100), (290, 64), (2, 0), (6, 8), -5.0),
     # a chunk boundary and a cut one token past it, 3 requests of 130-260
-    ("chunk boundaries", 2, (260, 130, 200), (128, 65, 200), (1, 4, 10), (11, 2, 3)),
-    # one long sequence on one head: pipelined scan segments (120 + 136 chunks),
-    # the checkpoint in the second segment
-    ("two segments", 1, (16384,), (9000,), (1,), (3,)),
+    ("chunk boundaries", 2, (260, 130, 200), (128, 65, 200), (1, 4, 10), (11, 2, 3), -5.0),
+    # one long sequence on one head: the affine form (eight segments of 32
+    # chunks), the checkpoint in the fifth
+    ("two segments", 1, (16384,), (9000,), (1,), (3,), -5.0),
+    # the same with weak decay (raw lower bound -2e-4): the checkpoint and the
+    # resumed suffix depend on the combined segment transitions
+    ("weak decay segments", 1, (16384,), (9000,), (1,), (3,), -2e-4),
+    # 16 heads: the pipelined scan segments (four of 64 chunks)
+    ("pipelined segments", 16, (16384,), (5000,), (1,), (3,), -5.0),
 ]
 
 
 @pytest.mark.parametrize("op", ["recurrent", "chunk"])
-@pytest.mark.parametrize("label,heads,lengths,cuts,slots,dests", CASES,
+@pytest.mark.parametrize("label,heads,lengths,cuts,slots,dests,lower_bound", CASES,
                          ids=[c[0].replace(" ", "-") for c in CASES])
 def test_tracking_is_invisible_and_resumes(gpu_ops, op, label, heads, lengths, cuts, slots,
-                                           dests):
+                                           dests, lower_bound):
     tracked_case = C.raw_case(heads, lengths, indices=list(slots), slots=SLOTS,
-                              seed=194195 + sum(lengths), track=(list(dests), list(cuts)))
+                              seed=194195 + sum(lengths), track=(list(dests), list(cuts)),
+                              lower_bound=lower_bound)
     plain_case = dataclasses.replace(tracked_case, track_indices=None, track_lens=None)
 
     # 1. tracking changes nothing but the destination slots
