@@ -87,6 +87,8 @@ REF_910B4_MS = {
     "decode H32 B1": 0.118, "decode H32 B32": 0.146, "decode H32 B128": 0.633,
     "decode H64 B1": 0.140, "decode H64 B32": 0.301, "decode H64 B128": 1.225,
     "verify 256K DP4TP2 R2": 0.03698,
+    # bench/kda_chunk/README.md:37-39 (kda_varlen_chunk, H8 C64, one sequence)
+    "chunk H8 T1k": 2.03, "chunk H8 T2k": 3.83, "chunk H8 T4k": 7.36,
 }
 
 
@@ -129,13 +131,16 @@ def settle(step, min_calls, max_calls=2000, batch=10, rel=0.01):
     return calls
 
 
-def timed(step, steps, warmup, min_settle):
-    """Settle, ``warmup`` untimed calls, then ``steps`` timed calls bracketed by
-    device synchronization. Returns wall ms per call, HIP-event µs per call on
-    the launch stream, and the settle call count."""
+def timed(step, steps, warmup, min_settle, before_timed=None):
+    """Settle, ``warmup`` untimed calls, ``before_timed()`` (untimed), then
+    ``steps`` timed calls bracketed by device synchronization. Returns wall ms
+    per call, HIP-event µs per call on the launch stream, and the settle call
+    count."""
     settle_calls = settle(step, min_settle)
     for _ in range(warmup):
         step()
+    if before_timed is not None:
+        before_timed()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -150,6 +155,38 @@ def timed(step, steps, warmup, min_settle):
     return dict(ms_per_step=(t1 - t0) * 1e3 / steps,
                 event_us_per_call=ev0.elapsed_time(ev1) * 1e3 / steps,
                 settle_calls=settle_calls)
+
+
+def graph_us(step, calls, replays=10):
+    """Per-call time of ``calls`` back-to-back calls captured in one HIP graph
+    and replayed ``replays`` times (HIP events on the replaying stream): the
+    device-side time of a call without the host's launch path, which sets
+    eager per-call times at small batch."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            step()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    ev1.record(stream)
+    ev1.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / (replays * calls)
+    del graph
+    return us
 
 
 # ---------------------------------------------------------------------------
@@ -319,6 +356,72 @@ def run_more(steps, warmup):
     return out
 
 
+# Raw-gate decode at config 2's shape: bytes per token-head (state in + out,
+# q, k, v, a bf16, b bf16, o bf16), plus A_log, dt_bias and the metadata.
+RAW_BYTES_PER_TOKEN_HEAD = 2 * DEC_D * DEC_D * 4 + 4 * DEC_D * 2 + 2 + DEC_D * 2
+RAW_DEC_BYTES = (DEC_N * DEC_H * RAW_BYTES_PER_TOKEN_HEAD + DEC_H * 4 + DEC_H * DEC_D * 4
+                 + (DEC_N + 1) * 4 + DEC_N * 4)
+
+
+def run_raw_decode(steps, warmup, min_settle, check):
+    """The sglang-facing ``kda_varlen_recurrent`` (raw gates: A_log, a,
+    dt_bias, b, lower_bound; q and k normalized in the kernel) at config 2's
+    shape: 256 sequences x 1 token, H=32, a 512-slot pool (randn*0.05, drawn on
+    the device), the seed-2 slot permutation. Validated on its first 64
+    sequences against the oracle, then timed."""
+    from oracle import kda_ref as R
+    from tests import kda_cases as C
+
+    ops = torch.ops.sgl_glm53_ascend
+    perm = torch.randperm(DEC_SLOTS, generator=C.gen(2))[:DEC_N].tolist()
+    case = C.raw_case(DEC_H, (1,) * DEC_N, slots=2, indices=perm, seed=21)
+    gen = torch.Generator(device="cuda").manual_seed(22)
+    pool = (torch.randn(DEC_SLOTS, DEC_H, DEC_D, DEC_D, generator=gen, device="cuda") * 0.05
+            ).transpose(-1, -2)
+    kw = case.kwargs("cuda", pool=pool)
+    validated = None
+    if check:
+        n = 64
+        before = pool[perm[:n]].cpu()
+        out = ops.kda_varlen_recurrent(prefill=False, **kw)
+        torch.cuda.synchronize()
+        ref_pool = torch.zeros(n + 1, DEC_H, DEC_D, DEC_D).transpose(-1, -2)
+        idx = []
+        for i, s_ in enumerate(perm[:n]):
+            if s_ > 0:
+                ref_pool[i + 1] = before[i]
+            idx.append(i + 1 if s_ > 0 else 0)
+        qn, kn, g, beta = R.kda_prepare(case.A_log, case.a[:, :n], case.dt_bias, case.q[:, :n],
+                                        case.k[:, :n], case.b[:, :n], case.lower_bound,
+                                        case.scale)
+        ref = R.kda_recurrent(qn, kn, case.v[:, :n], g, beta, state_pool=ref_pool,
+                              state_indices=torch.tensor(idx, dtype=torch.int32),
+                              cu_seqlens=torch.arange(n + 1, dtype=torch.int32),
+                              out_dtype=torch.float32)
+        got = torch.stack([pool[s_].cpu() if s_ > 0 else torch.zeros_like(ref_pool[0])
+                           for s_ in perm[:n]])
+        want = torch.stack([ref_pool[i] for i in idx])
+        validated = _errs(out[:, :n].cpu(), ref, got, want)
+        validated["sample"] = f"first {n} of {DEC_N} sequences"
+        validated["passed"] = _passed(validated)
+
+    def step():
+        return ops.kda_varlen_recurrent(prefill=False, **kw)
+
+    r = timed(step, steps, warmup, min_settle)
+    us = r["event_us_per_call"]
+    gbs = RAW_DEC_BYTES / (us * 1e-6) / 1e9
+    del pool
+    return dict(
+        workload=("kda_varlen_recurrent (raw gates, sglang schema) B=256 x 1 token, H=32, "
+                  "K=V=128, bf16 q/k/v/a/b, fp32 512-slot K-contiguous pool updated in place"),
+        tok_per_s=DEC_N / (r["ms_per_step"] / 1e3), ms_per_step=r["ms_per_step"],
+        event_us_per_call=us, settle_calls=r["settle_calls"], validated=validated,
+        roofline=dict(bound="hbm", achieved=gbs, peak=HBM_PEAK_GBS, unit="GB/s",
+                      frac=gbs / HBM_PEAK_GBS, algorithmic_bytes_per_launch=RAW_DEC_BYTES,
+                      kernel="recurrent_kernel<128,32,2,strided rows,decode,bf16,bf16,RAW>"))
+
+
 # ---------------------------------------------------------------------------
 # the CPU baseline leg: the oracle timed on the host, and as the checker
 # ---------------------------------------------------------------------------
@@ -419,32 +522,40 @@ def _passed(v):
 
 
 def latency_regimes():
-    """(label, heads, lengths, prefill, checkpoints), as the reference bench's
-    ``regimes()`` (bench_kda_varlen_recurrent.py:534-551) with its constants
-    (:77-114): decode H16/32/64 x B1/32/128; the verify shapes with 4 draft
-    tokens per request, checkpointed; recurrent prefill H4/H8 x T1k-16k."""
+    """(label, heads, lengths, prefill, checkpoints, op), as the reference
+    bench's ``regimes()`` (bench_kda_varlen_recurrent.py:534-551) with its
+    constants (:77-114): decode H16/32/64 x B1/32/128; the verify shapes with
+    4 draft tokens per request, checkpointed; recurrent prefill H4/H8 x
+    T1k-16k; and the reference chunk bench's rows (bench/kda_chunk/
+    bench_kda_chunk.py:420-467, README.md:37-39): ``kda_varlen_chunk`` at H8,
+    one sequence of 1k / 2k / 4k tokens."""
     for heads in (16, 32, 64):
         for batch in (1, 32, 128):
-            yield f"decode H{heads} B{batch}", heads, (1,) * batch, False, False
+            yield f"decode H{heads} B{batch}", heads, (1,) * batch, False, False, "recurrent"
     for label, heads, req in (("256K DP4TP2", 32, 2), ("256K DP2TP4", 16, 3),
                               ("256K DP8TP1", 64, 1), ("512K DP4TP2", 32, 1),
                               ("512K DP2TP4", 16, 1)):
-        yield f"verify {label} R{req}", heads, (4,) * req, False, True
+        yield f"verify {label} R{req}", heads, (4,) * req, False, True, "recurrent"
     for heads in (4, 8):
         for tokens in (1024, 2048, 4096, 8192, 16384):
-            yield f"prefill H{heads} T{tokens // 1024}k", heads, (tokens,), True, False
+            yield f"prefill H{heads} T{tokens // 1024}k", heads, (tokens,), True, False, "recurrent"
+    for tokens in (1024, 2048, 4096):
+        yield f"chunk H8 T{tokens // 1024}k", 8, (tokens,), True, False, "chunk"
 
 
 def run_latency_rows(steps, check):
     """Each regime through the sglang-facing op (raw gates, the reference
     bench's distributions), validated against the oracle when ``check`` (the
-    CPU leg is on), then timed."""
+    CPU leg is on), then timed twice: eagerly (HIP events around ``steps``
+    back-to-back calls, what a caller without graphs sees, host launch path
+    included) and as replays of a HIP graph of the same calls (the device
+    time per call)."""
     from oracle import kda_ref as R
     from tests import kda_cases as C
 
     ops = torch.ops.sgl_glm53_ascend
     rows = []
-    for label, heads, lengths, prefill, ckpt in latency_regimes():
+    for label, heads, lengths, prefill, ckpt, op in latency_regimes():
         case = C.raw_case(heads, lengths, seed=1000 + heads + len(lengths) + sum(lengths))
         N = len(lengths)
         D = 128
@@ -456,9 +567,12 @@ def run_latency_rows(steps, check):
         kw = case.kwargs("cuda", pool=pool)
 
         def step():
+            if op == "chunk":
+                return ops.kda_varlen_chunk(prefill=True, **kw)
             return ops.kda_varlen_recurrent(intermediate_state=mid_d, prefill=prefill, **kw)
 
-        row = dict(label=label, heads=heads, requests=N, tokens=int(sum(lengths)))
+        row = dict(label=label, op=f"kda_varlen_{op}", heads=heads, requests=N,
+                   tokens=int(sum(lengths)))
         if check:
             out = step()
             torch.cuda.synchronize()
@@ -466,9 +580,14 @@ def run_latency_rows(steps, check):
             ref_mid = None if mid is None else mid.transpose(-1, -2).clone().transpose(-1, -2)
             qn, kn, g, beta = R.kda_prepare(case.A_log, case.a, case.dt_bias, case.q, case.k,
                                             case.b, case.lower_bound, case.scale)
-            ref = R.kda_recurrent(qn, kn, case.v, g, beta, state_pool=ref_pool,
+            if op == "chunk":
+                ref = R.kda_chunk(qn, kn, case.v, g, beta, state_pool=ref_pool,
                                   state_indices=case.indices, cu_seqlens=case.cu_seqlens,
-                                  intermediate_state=ref_mid, out_dtype=torch.float32)
+                                  out_dtype=torch.float32)
+            else:
+                ref = R.kda_recurrent(qn, kn, case.v, g, beta, state_pool=ref_pool,
+                                      state_indices=case.indices, cu_seqlens=case.cu_seqlens,
+                                      intermediate_state=ref_mid, out_dtype=torch.float32)
             v = _errs(out.cpu(), ref, pool.cpu(), ref_pool)
             if ref_mid is not None:
                 v["checkpoint_err"] = C.max_rel_err(mid_d.cpu(), ref_mid)
@@ -485,9 +604,17 @@ def run_latency_rows(steps, check):
         row.update(event_us_per_call=us, settle_calls=r["settle_calls"],
                    hbm_gbs=nbytes / (us * 1e-6) / 1e9, algorithmic_bytes=nbytes,
                    ref_910b4_ms=REF_910B4_MS.get(label))
+        try:
+            gus = graph_us(step, 10 if not prefill else 2)
+            row.update(graph_us_per_call=gus, graph_hbm_gbs=nbytes / (gus * 1e-6) / 1e9)
+        except RuntimeError as e:  # reported, never fatal to the run
+            row.update(graph_us_per_call=None, graph_error=str(e)[:200])
+            gus = float("nan")
         rows.append(row)
         ok = row.get("validated", {}).get("passed", True)
-        _log(f"{label}: {us:.1f} us, {row['hbm_gbs']:.0f} GB/s{'' if ok else '  VALIDATION FAILED'}")
+        _log(f"{label}: {us:.1f} us eager, {gus:.1f} us graph, {row['hbm_gbs']:.0f} GB/s"
+             f"{'' if ok else '  VALIDATION FAILED'}")
+        del pool, mid_d
     return rows
 
 
@@ -628,6 +755,16 @@ def main():
              "settle calls")
         del pool, case
 
+    dec_raw = None
+    if not args.no_decode:
+        _log("decode, raw gates: config 2's shape through kda_varlen_recurrent")
+        dec_raw = run_raw_decode(args.steps, args.warmup, args.settle, check)
+        if dec_raw["validated"] is not None:
+            validated["decode_raw"] = dec_raw["validated"]
+            failed |= not dec_raw["validated"]["passed"]
+        _log(f"decode raw: {dec_raw['event_us_per_call']:.1f} us/call, "
+             f"{dec_raw['roofline']['frac'] * 100:.1f}% of HBM peak; {dec_raw['validated']}")
+
     prefill = None
     if not args.no_prefill:
         _log("prefill: config 3 (T=8192, H=32, K=V=128, chunk 64)")
@@ -655,13 +792,44 @@ def main():
             failed |= not ok
             _log(f"prefill validation: {validated['prefill']}{'' if ok else '  FAILED'}")
 
+        if check:
+            # the whole sequence: this call's output and final state (slot 1)
+            # against the recurrent kernel run in fp32 (bf16 inputs widened
+            # exactly), itself pinned to the oracle at 1e-5 by the tests
+            rpool = torch.zeros(2, PF_H, PF_D, PF_D, device="cuda").transpose(-1, -2)
+            rout = ops.kda_prepared_varlen_recurrent(
+                q.float(), k.float(), v.float(), g, beta, initial_state_source=rpool,
+                initial_state_indices=idx, cu_seqlens=cu, scale=case.scale)
+            torch.cuda.synchronize()
+            full = _errs(out.cpu(), rout.cpu(), pool[1].cpu(), rpool[1].cpu())
+            full["reference"] = ("this build's recurrent kernel with fp32 I/O over all 8192 tokens "
+                                 "(final state and every output row)")
+            validated["prefill_full"] = full
+            ok = _passed(full)
+            failed |= not ok
+            _log(f"prefill full-length check: {full}{'' if ok else '  FAILED'}")
+            del rpool, rout
+
+        # Every timed call starts from a zero state (config 3) and writes its
+        # final state: each takes its own slot of a pool zeroed before the
+        # timed calls, outside the timed region.
+        n_pf = max(5, args.steps // 2)
+        tpool = torch.zeros(n_pf + 1, PF_H, PF_D, PF_D, device="cuda").transpose(-1, -2)
+        tidx = [torch.tensor([i + 1], dtype=torch.int32, device="cuda") for i in range(n_pf)]
+        calls = [0]
+
         def pstep():
-            pool[1].zero_()  # zero initial state each step (config 3)
+            i = calls[0] % n_pf
+            calls[0] += 1
             return ops.kda_prepared_varlen_chunk(
-                q, k, v, g, beta, initial_state_source=pool, initial_state_indices=idx,
+                q, k, v, g, beta, initial_state_source=tpool, initial_state_indices=tidx[i],
                 cu_seqlens=cu, scale=case.scale)
 
-        pf = timed(pstep, max(5, args.steps // 2), args.warmup, (2 * args.settle) // 3)
+        def zero_slots():
+            tpool.zero_()
+            calls[0] = 0
+
+        pf = timed(pstep, n_pf, args.warmup, (2 * args.settle) // 3, before_timed=zero_slots)
         us = pf["event_us_per_call"]
         tf = PF_FLOP / (us * 1e-6) / 1e12
         traffic, traffic_src = traffic_from_profile("prefill_chunk_t8192_h32_hbm_traffic.md", pf_sha)
@@ -682,10 +850,12 @@ def main():
             traffic_source=traffic_src,
             source_sha256=pf_sha,
             workspace_bytes=int(sgl_glm53_ascend_ops.chunk_workspace_bytes(PF_T, 1, PF_H)),
+            timed_calls=("each from a zero state in its own slot of a pool zeroed before the "
+                         "timed calls (no fill inside the timed region)"),
             cpu_baseline=pf_cpu,
         )
         _log(f"prefill: {us:.1f} us/call, {tf:.1f} TFLOP/s after {pf['settle_calls']} settle calls")
-        del pool, case
+        del pool, case, tpool
 
     more = None
     rows = None
@@ -733,6 +903,7 @@ def main():
             event_us_per_call=dec["event_us_per_call"],
             source_sha256=dec_sha,
         ),
+        decode_raw=dec_raw,
         prefill=prefill,
         more_configs=more,
         latency_rows=rows,

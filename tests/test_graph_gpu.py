@@ -41,8 +41,8 @@ def _capture(fn):
 class _Inputs:
     """Static device buffers for q, k, v, a, b (refreshed in place) and the gate constants."""
 
-    def __init__(self, T, seed):
-        case = C.raw_case(H, (T,), D=D, seed=seed)
+    def __init__(self, T, seed, heads=H):
+        case = C.raw_case(heads, (T,), D=D, seed=seed)
         self.seed = seed
         self.const = dict(A_log=case.A_log.to(DEV), dt_bias=case.dt_bias.to(DEV),
                           lower_bound=case.lower_bound, scale=case.scale)
@@ -147,15 +147,17 @@ def test_prefill_tracking_graph_replay(gpu_ops, op):
         assert expected.float().abs().sum() > 0
 
 
-def test_chunk_two_segment_graph_replay(gpu_ops):
-    """One long sequence on few heads takes the chunk op's two-segment path
-    (a second stream forked and joined inside the op): captured once, replayed
-    with the slot (padding slot 0 included), the sequence bounds and the
-    tracked length moved across the segment boundary."""
+@pytest.mark.parametrize("heads", [4, 12], ids=["affine", "pipelined"])
+def test_chunk_two_segment_graph_replay(gpu_ops, heads):
+    """One long sequence on few heads: at 4 heads the chunk op's affine form
+    (four segments scanned at once, then combined), at 12 its pipelined
+    segments (a second stream forked and joined inside the op). Captured once
+    after eager calls, replayed with the slot (padding slot 0 included), the
+    sequence bounds and the tracked length moved across segment boundaries."""
     T = 16384
-    initial = C.to_dev(C.native_pool(6, H, D, seed=70), DEV)
+    initial = C.to_dev(C.native_pool(6, heads, D, seed=70), DEV)
     work, reference = C.clone_pool(initial), C.clone_pool(initial)
-    inp = _Inputs(T, seed=71)
+    inp = _Inputs(T, seed=71, heads=heads)
     slots = torch.tensor([1], dtype=torch.int32, device=DEV)
     dests = torch.tensor([4], dtype=torch.int32, device=DEV)
     cuts = torch.tensor([100], dtype=torch.int32, device=DEV)
