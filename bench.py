@@ -209,13 +209,13 @@ def source_sha256(names):
     return h.hexdigest()[:16]
 
 
-def profile_figures(name):
-    """The ``bench-figures: {...}`` JSON line of ``profiles/<name>`` or None."""
+def profile_figures(name, key="bench-figures"):
+    """The ``<key>: {...}`` JSON line of ``profiles/<name>`` or None."""
     path = os.path.join(PROFILES, name)
     try:
         with open(path) as f:
             for line in f:
-                m = re.match(r"\s*bench-figures:\s*(\{.*\})\s*$", line)
+                m = re.match(r"\s*" + re.escape(key) + r":\s*(\{.*\})\s*$", line)
                 if m:
                     return json.loads(m.group(1))
     except OSError:
@@ -223,14 +223,14 @@ def profile_figures(name):
     return None
 
 
-def traffic_from_profile(name, source):
+def traffic_from_profile(name, source, key="bench-figures"):
     """HBM bytes per launch from a counter summary: FETCH_SIZE and WRITE_SIZE
     KiB per dispatch, each scaled by what the same counter reads for a device
     copy of known size. None (and the reason) when the summary is missing or
     was measured on other kernel sources."""
-    fig = profile_figures(name)
+    fig = profile_figures(name, key)
     if fig is None:
-        return None, f"no bench-figures line in profiles/{name}"
+        return None, f"no {key} line in profiles/{name}"
     if fig.get("source_sha256") != source:
         return None, (f"profiles/{name} was measured on kernel sources "
                       f"{fig.get('source_sha256')}, these are {source}")
@@ -411,6 +411,8 @@ def run_raw_decode(steps, warmup, min_settle, check):
     r = timed(step, steps, warmup, min_settle)
     us = r["event_us_per_call"]
     gbs = RAW_DEC_BYTES / (us * 1e-6) / 1e9
+    traffic, traffic_src = traffic_from_profile("decode_recurrent_b256_h32_hbm_traffic.md",
+                                                source_sha256(DECODE_SOURCES), "bench-figures-raw")
     del pool
     return dict(
         workload=("kda_varlen_recurrent (raw gates, sglang schema) B=256 x 1 token, H=32, "
@@ -418,7 +420,8 @@ def run_raw_decode(steps, warmup, min_settle, check):
         tok_per_s=DEC_N / (r["ms_per_step"] / 1e3), ms_per_step=r["ms_per_step"],
         event_us_per_call=us, settle_calls=r["settle_calls"], validated=validated,
         roofline=dict(bound="hbm", achieved=gbs, peak=HBM_PEAK_GBS, unit="GB/s",
-                      frac=gbs / HBM_PEAK_GBS, algorithmic_bytes_per_launch=RAW_DEC_BYTES,
+                      frac=gbs / HBM_PEAK_GBS, traffic=traffic, traffic_source=traffic_src,
+                      algorithmic_bytes_per_launch=RAW_DEC_BYTES,
                       kernel="recurrent_kernel<128,32,2,strided rows,decode,bf16,bf16,RAW>"))
 
 
@@ -638,7 +641,8 @@ def summarize_trace(path, last):
     for (name, grid), xs in sorted(by.items(), key=lambda kv: -sum(u for _, u in kv[1])):
         xs.sort()
         sel = [u for _, u in (xs[-last:] if last > 0 else xs)]
-        print(f"| `{name[:100]}` | {grid} | {len(xs)} | {len(sel)} | {statistics.mean(sel):.2f} | "
+        short = re.sub(r"\(KdaRecurrentArgs\)|\(KdaChunkArgs[^)]*\)", "", name).replace("unsigned short", "u16")
+        print(f"| `{short[:150]}` | {grid} | {len(xs)} | {len(sel)} | {statistics.mean(sel):.2f} | "
               f"{statistics.median(sel):.2f} | {min(sel):.2f} | {max(sel):.2f} |")
 
 
@@ -653,7 +657,8 @@ def summarize_counters(path):
     print("| kernel | counter | dispatches | mean per dispatch |")
     print("|---|---|---|---|")
     for (name, ctr), xs in sorted(by.items()):
-        print(f"| `{name[:110]}` | {ctr} | {len(xs)} | {statistics.mean(xs):.1f} |")
+        short = re.sub(r"\(KdaRecurrentArgs\)|\(KdaChunkArgs[^)]*\)", "", name).replace("unsigned short", "u16")
+        print(f"| `{short[:150]}` | {ctr} | {len(xs)} | {statistics.mean(xs):.1f} |")
 
 
 # ---------------------------------------------------------------------------

@@ -227,7 +227,10 @@ int kda_chunk_launch(const KdaChunkArgs *args, void *workspace,
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). The workspace is a static device array of
  * KDA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; its address
- * on a device is resolved on the first call on that device. Several sequences
+ * on a device is resolved on the first call on that device. The array is part
+ * of the chunk kernels' code object: it occupies its 64 MiB on every GPU where
+ * this library's kernels are loaded, whether or not this entry point is
+ * called. Several sequences
  * whose records do not fit it (at K = V = 128 roughly 1190 (chunk, head)
  * pairs, e.g. 2 x 2048 tokens on 32 heads) return KDA_ERR_TOO_LARGE; a
  * single sequence of any length runs in windows of the chunks it holds (the
