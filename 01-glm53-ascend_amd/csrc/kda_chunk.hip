@@ -1269,6 +1269,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 //                     that stage's previous chunk j-1 finished before B1(j)),
 //                     then issue the loads of chunk j+3. The recurrence never
 //                     waits to issue a global load.
+// The affine form's first pass runs a lean variant: the chain waves load
+// their e^G k and (T^T kd)^T fragments, and the output waves their Aqk T,
+// from the record themselves a chunk ahead (every fragment has one reader
+// wave), and the loaders stage only v and the misc fragment. Its chains,
+// spread over the segments of one sequence, ran 6-11% faster so; the
+// one-pass and segmented scans are faster staged.
 // S_j, y_j and the stage are indexed by j's parity; a buffer of parity
 // j&1 is rewritten only after B1(j+1) or later, when its chunk-j readers are
 // done (the stage after B2(j+1): the output waves read its Aqk until then). One barrier B0 before the first chunk publishes
@@ -1289,6 +1295,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 // ---------------------------------------------------------------------------
 
 constexpr int kScanThreads = 768;
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt at their maxima: not waited for)
+constexpr int kWaitVm0 = 0x0F70;
 constexpr int kStKd = 16;  // stage fragment indices: e^G k at 0, (T^T kd)^T, Aqk T, then v
 constexpr int kStAq = 32;
 constexpr int kStV = 38;
@@ -1296,24 +1304,28 @@ static_assert(kOffKd == kStKd * kFrag && kOffAq == kStAq * kFrag && kOffQg == kS
                   kOffSc == kOffGl + DK * 4,
               "the stage copies the record's first 38 fragments in order, then gl and the scale block");
 
-// Stage of one chunk for NT column tiles: 38 shared fragments from the
-// record, this group's v as a row-major bf16 tile [64][16 NT] at fragment
-// kStV (loaded from the input; its region holds 4 NT fragments), then
-// e^(G_last) [128] and the scale block [128].
-template <int NT>
+// Stage of one chunk for NT column tiles. Staged form: 38 shared fragments
+// from the record, this group's v as a row-major bf16 tile [64][16 NT] at
+// fragment kStV (loaded from the input; its region holds 4 NT fragments),
+// then e^(G_last) [128] and the scale block [128]. Lean form (LEAN): the
+// record's matrix operands are loaded by the waves that use them (each
+// fragment has one reader), and the stage holds the v tile and the misc
+// fragment (e^(G_last) and the scale block) only.
+template <int NT, bool LEAN>
 struct Stage {
-    static constexpr int kFrags = kStV + 4 * NT + 1;
-    static constexpr int kMisc = (kStV + 4 * NT) * kFrag;
-    static constexpr int kRecFrags = kStV + 1;  // copied from the record: shared fragments, misc
-    static constexpr int kLoadPer = (kRecFrags + 3) / 4;  // record fragments per loader wave
+    static constexpr int kV = LEAN ? 0 : kStV * kFrag;  // byte offset of the v tile
+    static constexpr int kMisc = LEAN ? BT * 16 * NT * 2 : (kStV + 4 * NT) * kFrag;
+    static constexpr int kBytes = kMisc + kFrag;
+    static constexpr int kRecFrags = LEAN ? 1 : kStV + 1;  // copied from the record: shared fragments, misc
+    static constexpr int kLoadPer = (kRecFrags + 3) / 4;   // record fragments per loader wave
     // stage and record offsets of record fragment f (the last one is misc)
-    __device__ static int dst(int f) { return f < kStV ? f * kFrag : kMisc; }
-    __device__ static int src(int f) { return f < kStV ? f * kFrag : kOffGl; }
+    __device__ static int dst(int f) { return f < kRecFrags - 1 ? f * kFrag : kMisc; }
+    __device__ static int src(int f) { return f < kRecFrags - 1 ? f * kFrag : kOffGl; }
 };
 
-template <int NT>
+template <int NT, bool LEAN>
 struct ScanShared {
-    char stg[2][Stage<NT>::kFrags * kFrag];  // chain operands by parity, fragments in lane order
+    char stg[2][Stage<NT, LEAN>::kBytes];  // chain operands by parity, fragments in lane order
     u32x4 sbuf[2][4][NT][64];                // S_j as fp16 B fragments: [parity][slice][tile][lane]
     u32x4 vbuf[2][2][2][NT][64];             // y_j as fp16 B fragments: [parity][slice][hi, lo][tile][lane]
     float sscale[2][4];                      // 2^-shift of each S_j slice in sbuf
@@ -1321,7 +1333,7 @@ struct ScanShared {
     float vmax[2][4];                        // max |v| of each row tile of the staged v
     uint32_t otile[4][16][8 * NT];           // per output wave: 16 rows x CW bf16 columns
 };
-static_assert(sizeof(ScanShared<2>) <= 160 * 1024, "the scan's LDS budget");
+static_assert(sizeof(ScanShared<2, false>) <= 160 * 1024, "the scan's LDS budget");
 
 __device__ __forceinline__ f16x8 stage_frag(const char *st, int f, int lane) {
     return as_f16x8(reinterpret_cast<const u32x4 *>(st + f * kFrag)[lane]);
@@ -1362,11 +1374,15 @@ __device__ __forceinline__ void split_f16x2(float x0, float x1, int sh, uint32_t
 template <int NT, bool SEG, bool AFF = false>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws,
                                                                   int ring, int s_lo, int s_hi) {
-    using St = Stage<NT>;
+    // the affine first pass runs the lean form (its chains, spread over the
+    // segments of a long sequence, were measured faster loading their own
+    // operands; the one-sequence-per-chain scan is faster staged)
+    constexpr bool LEAN = AFF;
+    using St = Stage<NT, LEAN>;
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
     static_assert(!AFF || (NT == 1 && !SEG), "the affine pass scans 16-column groups of one sequence");
-    __shared__ ScanShared<NT> sm;
+    __shared__ ScanShared<NT, LEAN> sm;
 
     const int H = a.num_heads;
     const int N = a.num_seqs;
@@ -1546,7 +1562,28 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 
         // Chunk j's operands are read from the stage after B1(j) (the loaders
         // write it between B2(j-1) and B1(j)): those of phase B first, then
-        // those of phase C behind the first tile's S fragments.
+        // those of phase C behind the first tile's S fragments. In the lean
+        // form the matrix operands, e^G k (row tile wr) and (T^T kd)^T (row
+        // tiles 2wr, 2wr+1), are this wave's own loads from the record, a
+        // chunk ahead, into the register set chunk j-1 left.
+        struct OpsG {
+            f16x8 Kef[4];
+            f16x8 Kd[2][2];
+        };
+        auto load_g = [&](OpsG &op, int j) {
+            const u32x4 *rec = reinterpret_cast<const u32x4 *>(rec_of(j < j1 ? j : j1 - 1));
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                op.Kef[s] = as_f16x8(rec[(kOffKe / kFrag + wr * 4 + s) * 64 + lane]);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    op.Kd[tt][s] = as_f16x8(rec[(kOffKd / kFrag + (2 * wr + tt) * 2 + s) * 64 + lane]);
+                }
+            }
+        };
         struct OpsB {
             f16x8 Kef[4];
             f32x4 vv[NT];
@@ -1556,9 +1593,11 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         auto read_b = [&](OpsB &op, int j) {
             const char *st = sm.stg[j & 1];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
+            if constexpr (!LEAN) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                op.Kef[s] = stage_frag(st, wr * 4 + s, lane);
+                for (int s = 0; s < 4; ++s) {
+                    op.Kef[s] = stage_frag(st, wr * 4 + s, lane);
+                }
             }
             // v C tiles (rows 16 wr + 4gq + i, column 16 ct + r) from the
             // row-major bf16 tile: transposing reads, then widened
@@ -1567,7 +1606,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 const int g = lane >> 4;
                 const int m = (lane >> 2) & 3;
                 const int c4 = lane & 3;
-                const uint16_t *vt_tile = reinterpret_cast<const uint16_t *>(st + kStV * kFrag);
+                const uint16_t *vt_tile = reinterpret_cast<const uint16_t *>(st + St::kV);
                 const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                     (lds_s16x4 *)(vt_tile + (16 * wr + 4 * g + m) * CW + 16 * ct + 4 * c4));
 #pragma unroll
@@ -1580,11 +1619,14 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             op.kesc = *reinterpret_cast<const float4 *>(sc + kScKe + 4 * wr);
             op.kel1 = kel1_bound(sc);
         };
-        auto step = [&](int j) {
+        auto step = [&](int j, const OpsG &og, OpsG &next) {
             const int p = j & 1;
             const int len = eos - (bos + BT * j) < BT ? eos - (bos + BT * j) : BT;
             const char *st = sm.stg[p];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
+            if constexpr (LEAN) {
+                load_g(next, j + 1);
+            }
 
             // A. publish S_j (slice wr) as fp16 B fragments, scaled by a power
             // of two from the slice's largest magnitude (the state itself stays
@@ -1639,14 +1681,14 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 f32x4 acc[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    acc[s] = mfma(ob.Kef[s], as_f16x8(sm.sbuf[p][s][ct][lane]), z4);
+                    acc[s] = mfma(LEAN ? og.Kef[s] : ob.Kef[s], as_f16x8(sm.sbuf[p][s][ct][lane]), z4);
                 }
                 if (ct == 0) {
 #pragma unroll
                     for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
                         for (int s = 0; s < 2; ++s) {
-                            Kd[tt][s] = stage_frag(st, kStKd + (2 * wr + tt) * 2 + s, lane);
+                            Kd[tt][s] = LEAN ? og.Kd[tt][s] : stage_frag(st, kStKd + (2 * wr + tt) * 2 + s, lane);
                         }
                     }
 #pragma unroll
@@ -1732,9 +1774,29 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
         };
 
+        OpsG gA, gB;
+        if constexpr (LEAN) {
+            // the initial state's loads are waited for here, not at the loop's
+            // first use of S, where the wait would cover the prefetch too
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            if (j1 > j0) {
+                load_g(gA, j0);
+            }
+        }
         lds_barrier();  // B0: the first chunk's stage is written
-        for (int j = j0; j < j1; ++j) {
-            step(j);
+        if constexpr (LEAN) {
+            // chunk c's matrix operands are in gA when c - j0 is even, else gB
+            for (int j = j0; j < j1; j += 2) {
+                step(j, gA, gB);
+                if (j + 1 >= j1) {
+                    break;
+                }
+                step(j + 1, gB, gA);
+            }
+        } else {
+            for (int j = j0; j < j1; ++j) {
+                step(j, gA, gA);
+            }
         }
         if (j1 > j0) {
             lds_barrier();  // B1(j1)
@@ -1774,7 +1836,29 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // stage (rewritten only after B2(j+1)), y_j hi + lo from vbuf
         // (published before B2(j), rewritten after B1(j+2)), scaled as the
         // chain scaled it.
-        auto aqk_y = [&](int j) {
+        // q e^G rows [16wr, 16wr+16) and their scales (and in the lean form
+        // Aqk T rows [16wr, 16wr+16), which meet tokens >= 32 only for wr >=
+        // 2), loaded by this wave one chunk ahead (two sets; indices past the
+        // end clamped)
+        struct OpsO {
+            f16x8 Qg[4];
+            f16x8 Aq[2];
+            float4 qsc;
+        };
+        auto load_out = [&](OpsO &op, int j) {
+            const char *rec = rec_of(j < j1 ? j : j1 - 1);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                op.Qg[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffQg)[(wr * 4 + s) * 64 + lane]);
+            }
+            if constexpr (LEAN) {
+                const u32x4 *aq = reinterpret_cast<const u32x4 *>(rec + kOffAq);
+                op.Aq[0] = as_f16x8(aq[aq_frag(wr, 0) * 64 + lane]);
+                op.Aq[1] = as_f16x8(aq[aq_frag(wr, wr >= 2 ? 1 : 0) * 64 + lane]);
+            }
+            op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 4 * (kScQg + 4 * wr));
+        };
+        auto aqk_y = [&](const OpsO &op, int j) {
             const int p = j & 1;
             const char *st = sm.stg[p];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
@@ -1783,8 +1867,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             const int sv = f16_shift(max4_mag(um) + kel1_bound(sc) * max4_mag(sx));
             const float f = sc[kScAq + wr] * ldexpf(1.f, -sv);
             // rows [16wr, 16wr+16) meet tokens >= 32 only for wr >= 2
-            const f16x8 aq0 = stage_frag(st, kStAq + aq_frag(wr, 0), lane);
-            const f16x8 aq1 = stage_frag(st, kStAq + aq_frag(wr, wr >= 2 ? 1 : 0), lane);
+            const f16x8 aq0 = LEAN ? op.Aq[0] : stage_frag(st, kStAq + aq_frag(wr, 0), lane);
+            const f16x8 aq1 = LEAN ? op.Aq[1] : stage_frag(st, kStAq + aq_frag(wr, wr >= 2 ? 1 : 0), lane);
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
                 f32x4 acc = mfma(aq0, as_f16x8(sm.vbuf[p][0][0][ct][lane]), z4);
@@ -1854,30 +1938,24 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         };
-        // q e^G rows [16wr, 16wr+16) and their scales, loaded by this wave
-        // one chunk ahead (two sets; indices past the end clamped)
-        struct OpsO {
-            f16x8 Qg[4];
-            float4 qsc;
-        };
-        auto load_out = [&](OpsO &op, int j) {
-            const char *rec = rec_of(j < j1 ? j : j1 - 1);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                op.Qg[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffQg)[(wr * 4 + s) * 64 + lane]);
-            }
-            op.qsc = *reinterpret_cast<const float4 *>(rec + kOffSc + 4 * (kScQg + 4 * wr));
-        };
-        // Iteration j: [B1(j)] load chunk j+1 into `other`, form A of chunk
-        // j-1 and P = (q e^G) S_j from `cur` (fp16 q e^G against fp16 S_j,
+        // Iteration j: [B1(j)] load chunk j+1 into `other` and form A of chunk
+        // j-1 (in the lean form A first: `other` holds chunk j-1's Aqk T),
+        // then P = (q e^G) S_j from `cur` (fp16 q e^G against fp16 S_j,
         // one product per slice, then scaled; S_j's buffer is rewritten only
         // after B1(j+1)), [B2(j)] finish chunk j-1 (its P and A), keep P_j.
         auto iter = [&](const OpsO &cur, OpsO &other, int j) {
             const int p = j & 1;
             lds_barrier();  // B1(j)
-            load_out(other, j + 1);
-            if (j > j0) {
-                aqk_y(j - 1);
+            if constexpr (LEAN) {
+                if (j > j0) {
+                    aqk_y(other, j - 1);  // `other` still holds chunk j-1's Aqk T
+                }
+                load_out(other, j + 1);
+            } else {
+                load_out(other, j + 1);
+                if (j > j0) {
+                    aqk_y(other, j - 1);  // Aqk T from the stage
+                }
             }
             f32x4 Pn[NT];
             const float4 ss = *reinterpret_cast<const float4 *>(&sm.sscale[p][0]);
@@ -1922,7 +2000,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         }
         if (j1 > j0) {
             lds_barrier();  // B1(j1)
-            aqk_y(j1 - 1);
+            aqk_y(((j1 - 1 - j0) & 1) == 0 ? opA : opB, j1 - 1);
             finish(j1 - 1);
         }
     } else {
@@ -1988,7 +2066,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             for (int k = 0; k < kPer; ++k) {
                 reinterpret_cast<u32x4 *>(sm.stg[par] + St::dst(frag_of(k)))[lane] = R[k];
             }
-            uint16_t *vt_tile = reinterpret_cast<uint16_t *>(sm.stg[par] + kStV * kFrag);
+            uint16_t *vt_tile = reinterpret_cast<uint16_t *>(sm.stg[par] + St::kV);
             uint32_t m = 0;  // largest |v| as bf16 bits (order-preserving for magnitudes)
 #pragma unroll
             for (int k = 0; k < NT; ++k) {
