@@ -2605,11 +2605,12 @@ int window_chunks(int T) {
 // Its workspace keeps every record and two fp32 outputs per token, so it is
 // taken only while that stays within kAffMaxBytes (at 4 heads about 130,000
 // tokens); longer sequences keep the pipelined segments.
-// With two segments it does not pay (measured: 8 heads x 16384 tokens 321
-// against 312 us, 4 x 4096 96 against 80 us): the first pass's chains run
-// slower than the one-pass scan's, so it needs at least three.
+// Two segments pay only when they are long (measured: 8 heads x 16384
+// tokens 287 against 314 us for the pipelined scan, x 8192 141 against 161;
+// 4 x 4096, two segments of 32 chunks, 86 against 79 us one-pass), so P = 2
+// needs kAffMinChunksTwo chunks per segment.
 constexpr int kAffMinChunks = 32;
-constexpr int kAffMinSegments = 3;
+constexpr int kAffMinChunksTwo = 64;
 constexpr size_t kAffMaxBytes = size_t{1} << 30;
 
 int affine_segments(int T, int H, int cus, int &W) {
@@ -2621,7 +2622,7 @@ int affine_segments(int T, int H, int cus, int &W) {
         }
         P = p;
     }
-    if (P < kAffMinSegments || aff_layout(T, H, P).total > kAffMaxBytes) {
+    if (P < 2 || (P == 2 && (nch + 1) / 2 < kAffMinChunksTwo) || aff_layout(T, H, P).total > kAffMaxBytes) {
         P = 0;
     }
     W = P > 0 ? (nch + P - 1) / P : 0;

@@ -157,8 +157,9 @@ def test_chunk_workspace_size_formula(lib):
 
     A single sequence whose scan leaves most of a 256-CU device idle takes
     the affine form instead: P segments, the most for which its first pass's
-    8 (2P - 1) H workgroups fit the CUs with segments of at least 32 chunks,
-    when that is at least three and the total stays within 1 GiB. It keeps one record per chunk and
+    8 (2P - 1) H workgroups fit the CUs with segments of at least 32 chunks
+    (of at least 64 when that is two), when the total stays within 1 GiB.
+    It keeps one record per chunk and
     adds two fp32 outputs per token-head, and five sets of H 64 KiB states
     ((P - 1) each for the two scans' final states and the segment starts,
     one each for the two scans' tracked states)."""
@@ -185,7 +186,7 @@ def test_chunk_workspace_size_formula(lib):
         while 8 * H * (2 * p - 1) <= cus and (chunks + p - 1) // p >= 32:
             P = p
             p += 1
-        if P < 3:
+        if P < 2 or (P == 2 and (chunks + 1) // 2 < 64):
             return None
         outs = 2 * ((T * H * 512 + 255) // 256 * 256)
         one_pass = 256 + rec * (chunks + 1) * H + track * H + 65536 * H
@@ -194,12 +195,14 @@ def test_chunk_workspace_size_formula(lib):
 
     for T, N, H in [(8192, 1, 32), (33814, 16, 32), (65536, 1, 16), (65536, 1, 17), (16383, 1, 4),
                     (16384, 1, 4), (100000, 1, 8), (1, 1, 1), (0, 3, 2), (4096, 1, 8), (4095, 1, 8),
-                    (16384, 1, 1), (400000, 1, 4), (6144, 1, 4), (5952, 1, 4), (6144, 1, 6), (6144, 1, 7)]:
+                    (16384, 1, 1), (400000, 1, 4), (6144, 1, 4), (5952, 1, 4), (6144, 1, 6), (6144, 1, 7),
+                    (16384, 1, 8), (8192, 1, 8), (8191, 1, 8), (8065, 1, 7), (8064, 1, 7)]:
         expected = (affine(T, H) if N == 1 else None) or classic(T, N, H)
         assert lib.kda_chunk_workspace_bytes(T, N, H, 128) == expected, (T, N, H)
     # which shapes take the affine form
     assert affine(16384, 4) and affine(6144, 4) and affine(16384, 1) and affine(6144, 6)
-    assert not affine(65536, 16) and not affine(8192, 32) and not affine(16384, 8)
+    assert affine(16384, 8) and affine(8192, 8) and affine(8065, 7)  # two segments of >= 64 chunks
+    assert not affine(65536, 16) and not affine(8192, 32) and not affine(8064, 7)
     assert not affine(4096, 4) and not affine(6144, 7) and not affine(5952, 4)
     assert not affine(400000, 4) and not affine(100000, 8)  # beyond 1 GiB
 

@@ -35,7 +35,8 @@ SLOTS = 5
 # (label, heads, token bounds in a buffer of T tokens, T, slot, track (slot,
 # length), lower_bound). Segments on a 256-CU device: H=1 16384 tokens -> 8 x
 # 32 chunks; H=2 8192 -> 4 x 32; H=4 6144 -> 3 x 32; H=5 6144 -> 3 x 32;
-# H=6 6208 -> 3 x 33 chunks.
+# H=6 6208 -> 3 x 33 chunks; H=7 and H=8 8192 -> 2 x 64 (two segments need
+# at least 64 chunks each).
 # At lower_bound -5 (the raw gates' decay is then about -2.5 per token) a
 # segment's start barely reaches its outputs; at -2e-4 (about -1e-4 per
 # token, 0.2 nat over a 2048-token segment) every later output and the final
@@ -52,6 +53,9 @@ CASES = [
     ("weak decay H4 ragged, track on the boundary", 4, (11, 6144 - 30), 6144, 2, (3, 2048), -2e-4),
     ("weak decay H2 zero slot, track inside segment 3", 2, (0, 8192), 8192, 0, (3, 7001), -2e-4),
     ("weak decay H5", 5, (0, 6144), 6144, 1, (3, 4100), -2e-4),
+    ("H8 two segments, track in segment 1", 8, (0, 8192), 8192, 1, (3, 5000), -5.0),
+    ("weak decay H8 two segments, track on the boundary", 8, (0, 8192), 8192, 2, (3, 4096), -2e-4),
+    ("weak decay H7 ragged two segments", 7, (13, 8192 - 9), 8192, 1, (3, 100), -2e-4),
 ]
 
 

@@ -80,6 +80,9 @@ CASES = [
     ("weak decay segments", 1, (16384,), (9000,), (1,), (3,), -2e-4),
     # 16 heads: the pipelined scan segments (four of 64 chunks)
     ("pipelined segments", 16, (16384,), (5000,), (1,), (3,), -5.0),
+    # 8 heads: the affine form with two segments of 64 chunks, the checkpoint
+    # in the second
+    ("two affine segments", 8, (8192,), (5000,), (1,), (3,), -2e-4),
 ]
 
 
