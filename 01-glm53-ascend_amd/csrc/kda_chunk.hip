@@ -1527,21 +1527,39 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         }
-        // the tracked state's element: the pool's track slot, or the affine
-        // area of a later role
-        auto track_ptr = [&](int tt, int ct) {
-            if (AFF && trk_state != nullptr) {
-                return trk_state + static_cast<int64_t>(col0 + 16 * ct + r) * DK + 16 * (2 * wr + tt) + 4 * gq;
+        // Tile (tt, ct) of a later role's state into an affine area: [V][K]
+        // like the pool, except the identity-start role's, whose transitions
+        // go [K][V] (row k holds Phi[k][v'] for all v'), the layout the
+        // combine reads them in.
+        auto put_aff = [&](float *base, int tt, int ct, const f32x4 &val) {
+            const int k = 16 * (2 * wr + tt) + 4 * gq;
+            const int c = col0 + 16 * ct + r;
+            if (aff_phi) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    base[static_cast<int64_t>(k + i) * DK + c] = val[i];
+                }
+            } else {
+                *reinterpret_cast<float4 *>(base + static_cast<int64_t>(c) * DK + k) =
+                    make_float4(val[0], val[1], val[2], val[3]);
             }
-            return state_ptr(track_slot, tt, ct);
+        };
+        // the tracked state's tile: into the pool's track slot, or the
+        // affine area of a later role
+        auto put_track = [&](int tt, int ct, const f32x4 &val) {
+            if (AFF && trk_state != nullptr) {
+                put_aff(trk_state, tt, ct, val);
+            } else {
+                *reinterpret_cast<float4 *>(state_ptr(track_slot, tt, ct)) =
+                    make_float4(val[0], val[1], val[2], val[3]);
+            }
         };
         auto store_track = [&](const f32x4 (&val)[2][NT]) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
                 for (int ct = 0; ct < NT; ++ct) {
-                    *reinterpret_cast<float4 *>(track_ptr(tt, ct)) =
-                        make_float4(val[tt][ct][0], val[tt][ct][1], val[tt][ct][2], val[tt][ct][3]);
+                    put_track(tt, ct, val[tt][ct]);
                 }
             }
         };
@@ -1749,9 +1767,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                             tu = mfma(th, vl[s], tu);
                         }
                         const float f = tsc[2 * wr + tt] * inv_v;
-                        *reinterpret_cast<float4 *>(track_ptr(tt, ct)) =
-                            make_float4(S[tt][ct][0] * g2[0] + tu[0] * f, S[tt][ct][1] * g2[1] + tu[1] * f,
-                                        S[tt][ct][2] * g2[2] + tu[2] * f, S[tt][ct][3] * g2[3] + tu[3] * f);
+                        const f32x4 tv = {S[tt][ct][0] * g2[0] + tu[0] * f, S[tt][ct][1] * g2[1] + tu[1] * f,
+                                          S[tt][ct][2] * g2[2] + tu[2] * f, S[tt][ct][3] * g2[3] + tu[3] * f};
+                        put_track(tt, ct, tv);
                     }
                 }
 #pragma unroll
@@ -1806,9 +1824,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
                 for (int ct = 0; ct < NT; ++ct) {
-                    *reinterpret_cast<float4 *>(fin_state + static_cast<int64_t>(col0 + 16 * ct + r) * DK +
-                                                16 * (2 * wr + tt) + 4 * gq) =
-                        make_float4(S[tt][ct][0], S[tt][ct][1], S[tt][ct][2], S[tt][ct][3]);
+                    put_aff(fin_state, tt, ct, S[tt][ct]);
                 }
             }
         } else if (!last) {
@@ -2194,16 +2210,22 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 
 constexpr int kAffThreads = 256;
 
-// One workgroup per (head, 16 value columns): S_s for s = 1 .. P-1 (the true
-// state at each later segment's start, kept for the correction), the
-// tracked state when the tracked length ends inside a later segment (its
-// two tracked scan states combined the same way), and the final state into
-// the pool. Each 128 x 128 transition is staged in LDS with wide loads, then
-// multiplied in fp32, element k of a column summed over v' in order.
+// One workgroup per (head, 16 value columns), four waves: S_{s+1} = Phi_s
+// S_s + Z_s for s = 1 .. P-1 (S_1 is segment 0's final state, the carry
+// area), each S_s kept for the correction of segment s's outputs, the
+// tracked state when the tracked length ends inside a later segment (its two
+// tracked scan states combined the same way), and the final state into the
+// pool. The products run on the fp32 MFMA (v_mfma_f32_16x16x4f32, lane (r, g)
+// supplying A[r][g] and B[g][r] of each 4-wide K step, C as for the bf16
+// tiles) with the K index v' permuted: at step kk lane (r, g) supplies v' =
+// 32 g + kk, so its A values are 32 consecutive entries of a row of Phi
+// (stored [k][v'] by the identity-start scan) and its B values 32
+// consecutive entries of a column of S_s ([v'][k], the pool's layout). Every
+// wave holds all of S_s as B operands; wave w forms rows [32w, 32w + 32) of
+// S_{s+1}, and the new columns pass to the next step through LDS.
 __global__ __launch_bounds__(kAffThreads) void chunk_affine_combine_kernel(const KdaChunkArgs a, char *ws,
                                                                          int P, int W) {
-    __shared__ float mat[DK][DK];     // the staged transition, [v'][k] as stored
-    __shared__ float4 cur[2][DK][4];  // S_s columns: [buffer][v' = K index][16 columns as 4 float4]
+    __shared__ float sb[2][16][DK + 4];  // S_{s+1} by step parity: [column][k], rows padded
     const int H = a.num_heads;
     const int h = blockIdx.x >> 3;
     const int g = blockIdx.x & 7;
@@ -2236,112 +2258,114 @@ __global__ __launch_bounds__(kAffThreads) void chunk_affine_combine_kernel(const
     const size_t hoff = static_cast<size_t>(h) * DK * DK;
     auto area = [&](size_t off, int s) { return reinterpret_cast<float *>(ws + off + st * s) + hoff; };
     const int tid = threadIdx.x;
-    const int k = tid & (DK - 1);  // this thread's K row
-    const int vh = tid >> 7;       // its 8 columns: 16 g + 8 vh + e
-    const int col = 16 * g + 8 * vh;
-    // S_1 = segment 0's final state (the carry area, [V][K])
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15;
+    const int gq = lane >> 4;
+    const int col = 16 * g + r;  // this lane's column of S (B and C operands)
+    // S_s as B operands: bv[i][e] = S_s[32 gq + 4 i + e][col]; S_1 from the
+    // carry area ([V][K])
+    float4 bv[8];
     const float *carry = reinterpret_cast<const float *>(ws + LY.carry) + hoff;
-    for (int e = 0; e < 8; ++e) {
-        reinterpret_cast<float *>(&cur[0][k][2 * vh])[e] = carry[static_cast<int64_t>(col + e) * DK + k];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        bv[i] = load4(carry + static_cast<int64_t>(col) * DK + 32 * gq + 4 * i);
     }
-    // The transitions stream through `mat` (64 KiB, 16 float4 per thread):
-    // Phi_{s+1} and Z_{s+1} are loaded into registers while step s multiplies.
-    float4 rg[16];
-    float zz[8];
-    auto fetch = [&](const float *M, const float *Z) {
+    // A operands of this wave's two row tiles t: Phi[16 (2w + t) + r][32 gq + 4 i + e];
+    // C initial values: Z[16 (2w + t) + 4 gq + e][col]
+    struct Ops {
+        float4 A[2][8];
+        f32x4 Z[2];
+    };
+    auto fetch = [&](Ops &op, const float *M, const float *Z) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            rg[i] = reinterpret_cast<const float4 *>(M)[tid + kAffThreads * i];
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                op.A[t][i] = load4(M + static_cast<int64_t>(16 * (2 * w + t) + r) * DK + 32 * gq + 4 * i);
+            }
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            zz[e] = Z[static_cast<int64_t>(col + e) * DK + k];
+        for (int t = 0; t < 2; ++t) {
+            const float4 z = load4(Z + static_cast<int64_t>(col) * DK + 16 * (2 * w + t) + 4 * gq);
+            op.Z[t] = f32x4{z.x, z.y, z.z, z.w};
         }
     };
-    auto put = [&]() {
-        __syncthreads();  // every reader of the previous matrix is done
+    // out[t] = Z tile t + (Phi S_s) tile t: 32 K steps per tile, the two
+    // tiles' chains interleaved
+    auto product = [&](const Ops &op, f32x4 (&out)[2]) {
+        out[0] = op.Z[0];
+        out[1] = op.Z[1];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            reinterpret_cast<float4 *>(&mat[0][0])[tid + kAffThreads * i] = rg[i];
-        }
-        __syncthreads();
-    };
-    // acc[e] += sum_v' mat[v'][k] cur[v'][col + e]
-    auto product = [&](int b, float (&acc)[8]) {
-#pragma unroll 8
-        for (int v2 = 0; v2 < DK; ++v2) {
-            const float m = mat[v2][k];
-            const float4 c0 = cur[b][v2][2 * vh];
-            const float4 c1 = cur[b][v2][2 * vh + 1];
-            acc[0] = fmaf(m, c0.x, acc[0]);
-            acc[1] = fmaf(m, c0.y, acc[1]);
-            acc[2] = fmaf(m, c0.z, acc[2]);
-            acc[3] = fmaf(m, c0.w, acc[3]);
-            acc[4] = fmaf(m, c1.x, acc[4]);
-            acc[5] = fmaf(m, c1.y, acc[5]);
-            acc[6] = fmaf(m, c1.z, acc[6]);
-            acc[7] = fmaf(m, c1.w, acc[7]);
+        for (int i = 0; i < 8; ++i) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                out[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(op.A[t][i].x, bv[i].x, out[t], 0, 0, 0);
+                out[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(op.A[t][i].y, bv[i].y, out[t], 0, 0, 0);
+                out[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(op.A[t][i].z, bv[i].z, out[t], 0, 0, 0);
+                out[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(op.A[t][i].w, bv[i].w, out[t], 0, 0, 0);
+            }
         }
     };
     const int64_t head_off = static_cast<int64_t>(h) * a.state_stride_head;
-    auto pool_col = [&](int s_, int e) {
-        return a.state + s_ * a.state_stride_slot + head_off + static_cast<int64_t>(col + e) * DK + k;
-    };
-    int b = 0;
-    fetch(area(AL.fin_phi, 0), area(AL.fin_zero, 0));
-    for (int s = 1; s < P && s * W < nch; ++s) {
-        // S_s, kept for the correction of segment s's outputs
-        float *start = area(AL.start, s - 1);
-        for (int e = 0; e < 8; ++e) {
-            start[static_cast<int64_t>(col + e) * DK + k] = reinterpret_cast<const float *>(&cur[b][k][2 * vh])[e];
+    // this wave's quarter of a state held as B operands (rows 32 gq + 4 i,
+    // i = 2 (w & 3) .. +1), into [V][K] at `dst`
+    auto store_b = [&](float *dst) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if ((i >> 1) == w) {
+                *reinterpret_cast<float4 *>(dst + static_cast<int64_t>(col) * DK + 32 * gq + 4 * i) = bv[i];
+            }
         }
-        // a tracked length inside segment s: tokens (64 s W, min(64 (s+1) W, len)]
-        // (at most one segment holds it: its two tracked states pass through
-        // `mat` first, Phi_s's loads waiting in registers)
+    };
+    // one step: S_s kept, the tracked state if it ends in segment s, the
+    // next transition's loads issued into `nxt`, then S_{s+1} into bv
+    auto step = [&](int s, const Ops &cur, Ops &nxt) {
+        store_b(area(AL.start, s - 1));
         const int seg_end = (s + 1) * W < nch ? BT * (s + 1) * W : eos - bos;
         if (track_slot > 0 && track_len > BT * s * W && track_len <= seg_end) {
-            const float *tphi = reinterpret_cast<const float *>(ws + AL.trk_phi) + hoff;
-            const float *tz = reinterpret_cast<const float *>(ws + AL.trk_zero) + hoff;
-            float4 tr[16];
+            Ops tr;
+            fetch(tr, reinterpret_cast<const float *>(ws + AL.trk_phi) + hoff,
+                  reinterpret_cast<const float *>(ws + AL.trk_zero) + hoff);
+            f32x4 tv[2];
+            product(tr, tv);
+            float *pool = a.state + track_slot * a.state_stride_slot + head_off;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                tr[i] = reinterpret_cast<const float4 *>(tphi)[tid + kAffThreads * i];
+            for (int t = 0; t < 2; ++t) {
+                *reinterpret_cast<float4 *>(pool + static_cast<int64_t>(col) * DK + 16 * (2 * w + t) + 4 * gq) =
+                    make_float4(tv[t][0], tv[t][1], tv[t][2], tv[t][3]);
             }
-            float acc[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                acc[e] = tz[static_cast<int64_t>(col + e) * DK + k];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                reinterpret_cast<float4 *>(&mat[0][0])[tid + kAffThreads * i] = tr[i];
-            }
-            __syncthreads();
-            product(b, acc);
-            for (int e = 0; e < 8; ++e) {
-                *pool_col(track_slot, e) = acc[e];
-            }
-        }
-        put();  // Phi_s into mat
-        float acc[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            acc[e] = zz[e];
         }
         if (s + 1 < P && (s + 1) * W < nch) {
-            fetch(area(AL.fin_phi, s), area(AL.fin_zero, s));
+            fetch(nxt, area(AL.fin_phi, s), area(AL.fin_zero, s));
         }
-        product(b, acc);
-        for (int e = 0; e < 8; ++e) {
-            reinterpret_cast<float *>(&cur[b ^ 1][k][2 * vh])[e] = acc[e];
+        f32x4 out[2];
+        product(cur, out);
+        float(*buf)[DK + 4] = sb[s & 1];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            *reinterpret_cast<float4 *>(&buf[r][16 * (2 * w + t) + 4 * gq]) =
+                make_float4(out[t][0], out[t][1], out[t][2], out[t][3]);
         }
-        b ^= 1;  // the next put's first barrier orders these writes before any read
+        // one barrier per step: the buffer this step wrote is rewritten two
+        // steps later, after every wave has passed the next step's barrier
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            bv[i] = *reinterpret_cast<const float4 *>(&buf[r][32 * gq + 4 * i]);
+        }
+    };
+    Ops oa, ob;
+    fetch(oa, area(AL.fin_phi, 0), area(AL.fin_zero, 0));
+    for (int s = 1; s < P && s * W < nch; s += 2) {
+        step(s, oa, ob);
+        if (s + 1 >= P || (s + 1) * W >= nch) {
+            break;
+        }
+        step(s + 1, ob, oa);
     }
     if (slot > 0) {
-        for (int e = 0; e < 8; ++e) {
-            *pool_col(slot, e) = reinterpret_cast<const float *>(&cur[b][k][2 * vh])[e];
-        }
+        store_b(a.state + slot * a.state_stride_slot + head_off);
     }
 }
 
