@@ -183,8 +183,8 @@ typedef struct KdaChunkArgs {
  * possible chunk and head, or, for a single sequence of at least 16384 tokens
  * on at most 16 heads, a ring of two scan segments' records per head), the
  * tracking records and, when N == 1, the state carried between scan
- * segments. A single sequence that takes the affine form (at most 6 heads on
- * 256 CUs, at least 3 segments of 32 chunks, at most 1 GiB in all) needs one
+ * segments. A single sequence that takes the affine form (at most 8 heads on
+ * 256 CUs, at least 3 segments of 32 chunks or 2 of 64, at most 1 GiB in all) needs one
  * record per chunk, two fp32 outputs per token-head and 3 (P - 1) + 2 sets of
  * H fp32 128 x 128 states besides; with less than that but at least the other forms'
  * size, kda_chunk_launch runs those. */
