@@ -16,7 +16,9 @@ Also reported in the same JSON line:
 * ``roofline`` -- the decode kernel: algorithmic bytes / HIP-event time per
   call on the launch stream; ``traffic`` is the HBM bytes per launch from the
   committed rocprofv3 counter summary, used only while the kernel source it was
-  measured on is unchanged (``source_sha256`` in the summary);
+  measured on is unchanged (``source_sha256`` in the summary); ``copy_gbs`` is
+  what a plain 512 MiB device-to-device copy reaches on the same GPU (bytes read
+  plus written per time), a reference for the achievable streaming rate;
 * ``more_configs`` -- configs 4 and 5 (prefill) and config 5's 4-token decode;
 * ``latency_rows`` -- the reference bench's deployed shapes
   (bench/kda_recurrent/bench_kda_varlen_recurrent.py:81-114,534-551): decode
@@ -626,6 +628,28 @@ def run_latency_rows(steps, check):
 # ---------------------------------------------------------------------------
 
 
+def copy_gbs(mib=512, calls=10):
+    """Read + write bytes per second of a plain device-to-device copy of `mib`
+    MiB (torch's copy kernel), best of `calls`, timed with HIP events."""
+    n = mib * 2 ** 20 // 4
+    src = torch.ones(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = float("inf")
+    for _ in range(calls):
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1))
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * n * 4 / (best * 1e-3) / 1e9
+
+
 def summarize_trace(path, last):
     """Per-kernel duration statistics from a rocprofv3 kernel-trace CSV, one
     row per (kernel, grid size) -- the grid tells the workloads of one kernel
@@ -878,6 +902,9 @@ def main():
     tok_s = DEC_N / (dec["ms_per_step"] / 1e3)
     achieved = DEC_BYTES / (dec["event_us_per_call"] * 1e-6) / 1e9
     traffic, traffic_src = traffic_from_profile("decode_recurrent_b256_h32_hbm_traffic.md", dec_sha)
+    copy_ref = copy_gbs()
+    _log(f"reference: a 512 MiB device copy reaches {copy_ref:.0f} GB/s (read + write); "
+         f"the decode {achieved:.0f} GB/s")
     line = dict(
         metric="KDA decode tok/s + state HBM GB/s (B=256); chunk prefill tok/s (T=8k)",
         value=tok_s,
@@ -907,6 +934,7 @@ def main():
             algorithmic_bytes_per_launch=DEC_BYTES,
             event_us_per_call=dec["event_us_per_call"],
             source_sha256=dec_sha,
+            copy_gbs=copy_ref,
         ),
         decode_raw=dec_raw,
         prefill=prefill,
