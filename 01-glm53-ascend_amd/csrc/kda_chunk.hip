@@ -242,48 +242,39 @@ __device__ __forceinline__ f16x8 to_f16x8(const float x[8], int sh) {
     }
     return h;
 }
-// x * 2^sh = hi + lo to about 2^-22 relative (fp16, round to nearest even),
-// converted in pairs (one packed conversion per two values)
-__device__ __forceinline__ void split_f16x8(const float x[8], int sh, f16x8 &hi, f16x8 &lo) {
+// (x0, x1) * 2^sh = hi + lo to about 2^-22 relative, as packed fp16 pairs
+// (round to nearest even; bits of x0 in the low half): one packed conversion
+// for the high parts, the exact residuals xs - hi with hi read as fp16 from
+// its half of the packed pair (v_fma_mix_f32), one packed conversion for the
+// low parts.
+__device__ __forceinline__ void split_f16x2(float x0, float x1, int sh, uint32_t &hi, uint32_t &lo) {
     typedef float f32x2_t __attribute__((ext_vector_type(2)));
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t xs = {ldexpf(x0, sh), ldexpf(x1, sh)};
+    const f16x2_t h = __builtin_convertvector(xs, f16x2_t);
+    const uint32_t hp = __builtin_bit_cast(uint32_t, h);
+    float d0, d1;
+    asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,0] op_sel_hi:[0,0,1]" : "=v"(d0) : "v"(xs[0]), "v"(hp));
+    asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(d1) : "v"(xs[1]), "v"(hp));
+    const f32x2_t ds = {d0, d1};
+    hi = hp;
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(ds, f16x2_t));
+}
+// the same for eight values
+__device__ __forceinline__ void split_f16x8(const float x[8], int sh, f16x8 &hi, f16x8 &lo) {
+    uint32_t h[4], l[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const f32x2_t xs = {ldexpf(x[2 * p], sh), ldexpf(x[2 * p + 1], sh)};
-        const f16x2_t h = __builtin_convertvector(xs, f16x2_t);
-        // xs - hi, exact, with hi read as fp16 from its half of the packed pair
-        const uint32_t hp = __builtin_bit_cast(uint32_t, h);
-        float d0, d1;
-        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,0] op_sel_hi:[0,0,1]"
-            : "=v"(d0) : "v"(xs[0]), "v"(hp));
-        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-            : "=v"(d1) : "v"(xs[1]), "v"(hp));
-        const f32x2_t ds = {d0, d1};
-        const f16x2_t l = __builtin_convertvector(ds, f16x2_t);
-        hi[2 * p] = h[0];
-        hi[2 * p + 1] = h[1];
-        lo[2 * p] = l[0];
-        lo[2 * p + 1] = l[1];
+        split_f16x2(x[2 * p], x[2 * p + 1], sh, h[p], l[p]);
     }
+    hi = __builtin_bit_cast(f16x8, u32x4{h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(f16x8, u32x4{l[0], l[1], l[2], l[3]});
 }
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 __device__ __forceinline__ u32x4 as_u32x4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
 
 __device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// Largest x over the wave, in every lane.
-__device__ __forceinline__ float wave_max(float x) {
-    x = fmaxf(x, dpp_mov<kDppQuadXor1>(x));
-    x = fmaxf(x, dpp_mov<kDppQuadXor2>(x));
-    x = fmaxf(x, dpp_mov<kDppRowHalfMirror>(x));
-    x = fmaxf(x, dpp_mov<kDppRowMirror>(x));
-    const float a = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)),
-                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16)));
-    const float b = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32)),
-                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48)));
-    return fmaxf(a, b);
 }
 
 // Largest value over the wave for nonnegative x (magnitudes and sums of
@@ -1337,21 +1328,6 @@ static_assert(sizeof(ScanShared<2, false>) <= 160 * 1024, "the scan's LDS budget
 
 __device__ __forceinline__ f16x8 stage_frag(const char *st, int f, int lane) {
     return as_f16x8(reinterpret_cast<const u32x4 *>(st + f * kFrag)[lane]);
-}
-
-__device__ __forceinline__ uint32_t f16_bits2(_Float16 a, _Float16 b) {
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
-}
-// (x0, x1) * 2^sh = hi + lo as packed fp16 pairs
-__device__ __forceinline__ void split_f16x2(float x0, float x1, int sh, uint32_t &hi, uint32_t &lo) {
-    const float a0 = ldexpf(x0, sh);
-    const float a1 = ldexpf(x1, sh);
-    const _Float16 h0 = static_cast<_Float16>(a0);
-    const _Float16 h1 = static_cast<_Float16>(a1);
-    hi = f16_bits2(h0, h1);
-    lo = f16_bits2(static_cast<_Float16>(a0 - static_cast<float>(h0)),
-                   static_cast<_Float16>(a1 - static_cast<float>(h1)));
 }
 
 // SEG: one segment [s_lo, s_hi) of a single sequence's chunks (the state
