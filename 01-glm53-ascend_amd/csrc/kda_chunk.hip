@@ -134,6 +134,7 @@ static_assert(kRecBytes % 256 == 0 && kTrBytes % 256 == 0, "records stay 256-B a
 
 struct Layout {
     size_t chunk_start;  // int32 [N+1]
+    size_t sched;        // several sequences: int4 [2N+1], see chunk_index_kernel
     size_t recs;         // kRecBytes x (ring x H): chunk c's record in ring slot c % ring
     size_t tracks;       // kTrBytes x (N x H)
     size_t carry;        // one sequence: fp32 [H][V][K], the state between scan segments
@@ -153,7 +154,8 @@ __host__ __device__ constexpr int aq_frag(int mt, int s) { return mt < 2 ? mt : 
 __host__ __device__ inline Layout layout(int T, int N, int H, int ring) {
     Layout L;
     L.chunk_start = 0;
-    L.recs = align256(static_cast<size_t>(N + 1) * 4);
+    L.sched = align256(static_cast<size_t>(N + 1) * 4);
+    L.recs = N > 1 ? L.sched + align256(static_cast<size_t>(2 * N + 1) * 16) : L.sched;
     L.tracks = L.recs + static_cast<size_t>(kRecBytes) * ring * H;
     L.carry = L.tracks + static_cast<size_t>(kTrBytes) * N * H;
     L.total = L.carry + (N == 1 ? static_cast<size_t>(DK) * DK * 4 * H : 0);
@@ -368,11 +370,23 @@ __device__ __forceinline__ void seq_bounds(const KdaChunkArgs &a, int n, int &bo
 }
 
 // ---------------------------------------------------------------------------
-// K0: chunk_start[n] = sum_{m<n} ceil(len_m / 64), chunk_start[N] = total.
+// K0 (several sequences): chunk_start[n] = sum_{m<n} ceil(len_m / 64),
+// chunk_start[N] = total; with `sort` (the persistent scan runs next), also
+// the sequences ordered by chunk count, longest first (ties by index): for
+// rank r < N, sched[2r] = (n, chunk_start[n], bos_n, eos_n) and sched[2r+1]
+// = (pool slot, tracked slot, tracked length, 0) with the slots' range rules
+// applied (0: none; length -1: no tracking), and sched[2N].x = the number of
+// nonempty sequences (a prefix of that order).
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a, int *cs) {
+// Sequences the schedule sorts (in LDS) at most, and items per persistent
+// team at most; beyond either the scan runs a workgroup per item.
+constexpr int kPersMaxSeqs = 4096;
+constexpr int kPersMaxItems = 256;
+
+__global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a, int *cs, int4 *sched, int sort) {
     __shared__ int part[1024];
+    __shared__ unsigned long long key[kPersMaxSeqs];
     const int N = a.num_seqs;
     const int tid = threadIdx.x;
     const int per = (N + 1023) / 1024;
@@ -401,6 +415,69 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
     }
     if (tid == 1023) {
         cs[N] = part[1023];
+    }
+    if (sort == 0 || N > kPersMaxSeqs) {
+        return;
+    }
+    // bitonic sort, descending, of (chunks + 1, ~n): padding (zero) sorts
+    // after every sequence, empty ones included
+    int npad = 1;
+    while (npad < N) {
+        npad <<= 1;
+    }
+    for (int i = tid; i < npad; i += 1024) {
+        unsigned long long kk = 0;
+        if (i < N) {
+            int bos, eos;
+            seq_bounds(a, i, bos, eos);
+            const unsigned c = static_cast<unsigned>((eos - bos + BT - 1) / BT);
+            kk = (static_cast<unsigned long long>(c + 1) << 32) | (0xffffffffu - static_cast<unsigned>(i));
+        }
+        key[i] = kk;
+    }
+    __syncthreads();  // also orders every thread's chunk_start stores before the reads below
+    for (int size = 2; size <= npad; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < npad; i += 1024) {
+                const int pj = i ^ stride;
+                if (pj > i) {
+                    const bool desc = (i & size) == 0;
+                    const unsigned long long x = key[i];
+                    const unsigned long long y = key[pj];
+                    if (desc ? x < y : x > y) {
+                        key[i] = y;
+                        key[pj] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int r = tid; r < N; r += 1024) {
+        const int n = static_cast<int>(0xffffffffu - static_cast<unsigned>(key[r] & 0xffffffffu));
+        int bos, eos;
+        seq_bounds(a, n, bos, eos);
+        int slot = a.state_indices[n];
+        if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
+            slot = 0;
+        }
+        int tslot = 0;
+        int tlen = -1;
+        if (a.track_indices != nullptr) {
+            tslot = a.track_indices[n];
+            if (tslot <= 0 || static_cast<int64_t>(tslot) >= a.num_slots) {
+                tslot = 0;
+            } else {
+                tlen = a.track_lens[n];
+            }
+        }
+        sched[2 * r] = make_int4(n, cs[n], bos, eos);
+        sched[2 * r + 1] = make_int4(slot, tslot, tlen, 0);
+        const bool nonempty = (key[r] >> 32) > 1;
+        const bool next_empty = r + 1 == N || (key[r + 1] >> 32) <= 1;
+        if ((nonempty && next_empty) || (r == 0 && !nonempty)) {
+            sched[2 * N] = make_int4(nonempty ? r + 1 : 0, 0, 0, 0);
+        }
     }
 }
 
@@ -1347,7 +1424,19 @@ __device__ __forceinline__ f16x8 stage_frag(const char *st, int f, int lane) {
 // later roles write fp32 outputs and their final and tracked states to the
 // affine areas; chunk_affine_combine_kernel and chunk_affine_correct_kernel
 // finish the sequence.
-template <int NT, bool SEG, bool AFF = false>
+//
+// PERS: one pass over several sequences with one workgroup per CU. The
+// workgroups form teams of NV (one per column group, on one XCD); team t of
+// TM takes the (sequence, head) items of ranks k TM + t (k even) and k TM +
+// TM - 1 - t (k odd) in the order chunk_index_kernel sorted them (longest
+// first, so the teams' loads balance), and runs their chunks as one stream:
+// virtual chunk J is local chunk j of item k. The loaders' look-ahead, the
+// output waves' lag and the stage parity (J & 1) run across items, so an
+// item's first chunks are staged while the previous one finishes, and the
+// chain loads the next item's initial state a whole item ahead; what a
+// workgroup per item paid at its start (about 3.9 us: dispatch, the first
+// loads, the pipeline's fill and drain) is paid once per workgroup.
+template <int NT, bool SEG, bool AFF = false, bool PERS = false>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunkArgs a, const char *ws,
                                                                   int ring, int s_lo, int s_hi) {
     // the affine first pass runs the lean form (its chains, spread over the
@@ -1358,7 +1447,16 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     constexpr int NV = 8 / NT;  // column groups per (sequence, head)
     constexpr int CW = 16 * NT;
     static_assert(!AFF || (NT == 1 && !SEG), "the affine pass scans 16-column groups of one sequence");
+    static_assert(!PERS || (!SEG && !AFF), "the persistent scan is one pass over several sequences");
     __shared__ ScanShared<NT, LEAN> sm;
+    // PERS: the team's items ((n << 16 | h, first record chunk, bos, eos),
+    // (pool slot, tracked slot, tracked length, 0)), the nonempty ones first;
+    // the chunk total of those; the items of sequences
+    // 0 and N - 1 (a bit per item), which also write the rows outside every
+    // sequence
+    __shared__ int4 items[PERS ? kPersMaxItems : 1][2];
+    __shared__ int item_chunks[1];
+    __shared__ uint32_t edge_items[PERS ? kPersMaxItems / 32 : 1];
 
     const int H = a.num_heads;
     const int N = a.num_seqs;
@@ -1369,8 +1467,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     const int xcd = b & 7;
     const int rest = b >> 3;
     const int vt = rest % NV;
-    const int pair = (rest / NV) * 8 + xcd;
-    if (pair >= pairs) {
+    const int pair = (rest / NV) * 8 + xcd;  // PERS: the team
+    if (!PERS && pair >= pairs) {
         return;
     }
     // AFF: the chain's role (0: segment 0; 2s - 1: zero start, 2s: identity
@@ -1378,8 +1476,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     const int role = AFF ? pair / H : 0;
     const bool aff_zero = AFF && (role & 1) != 0;
     const bool aff_phi = AFF && role > 0 && (role & 1) == 0;
-    const int n = AFF ? 0 : pair / H;
-    const int h = AFF ? pair - role * H : pair - n * H;
+    // PERS: set per item by each role
+    int n = AFF || PERS ? 0 : pair / H;
+    int h = AFF ? pair - role * H : PERS ? 0 : pair - n * H;
     const Layout LY = layout(a.num_tokens, N, H, ring);
     const int *cs = reinterpret_cast<const int *>(ws + LY.chunk_start);
     int bos, eos;
@@ -1434,6 +1533,82 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     float *carry = reinterpret_cast<float *>(const_cast<char *>(ws) + LY.carry) +
                    static_cast<size_t>(h) * DK * DK;
 
+    // PERS: the team's item table (KA items, the first KT nonempty) and the
+    // stream's length; every role derives its loop and barrier count from it
+    int KT = 0;
+    int KA = 0;
+    if constexpr (PERS) {
+        const int TM = static_cast<int>(gridDim.x) / NV;
+        const int t = pair;
+        const int4 *sched = reinterpret_cast<const int4 *>(ws + LY.sched);
+        // items of ranks below X: all k < X / TM, and k = X / TM if its rank is
+        auto count = [&](int X) {
+            const int q = X / TM;
+            const int off = (q & 1) ? TM - 1 - t : t;
+            return q + (off < X - q * TM ? 1 : 0);
+        };
+        KA = count(N * H);
+        KT = count(sched[2 * N].x * H);
+        const int tk = static_cast<int>(threadIdx.x);
+        if (tk == 0) {
+            item_chunks[0] = 0;
+        }
+        if (tk < kPersMaxItems / 32) {
+            edge_items[tk] = 0u;
+        }
+        __syncthreads();
+        if (tk < KA) {
+            const int rk = tk * TM + ((tk & 1) ? TM - 1 - t : t);
+            const int4 e = sched[2 * (rk / H)];
+            items[tk][0] = make_int4((e.x << 16) | (rk % H), e.y, e.z, e.w);
+            items[tk][1] = sched[2 * (rk / H) + 1];
+            if (tk < KT) {
+                atomicAdd(&item_chunks[0], (e.w - e.z + BT - 1) / BT);
+            }
+            if (e.x == 0 || e.x == N - 1) {
+                atomicOr(&edge_items[tk >> 5], 1u << (tk & 31));
+            }
+        }
+        __syncthreads();
+        j0 = 0;
+        j1 = item_chunks[0];
+    }
+    // PERS: a role's position in the stream: item k (virtual chunks [base,
+    // base + nch)) of sequence n and head h, its first record chunk c0 and
+    // tokens [bos, eos)
+    struct Cur {
+        int base, k, nch, n, h, c0, bos, eos;
+    };
+    auto cur_load = [&](Cur &c, int k) {
+        const int4 e = items[k][0];
+        c.k = k;
+        c.n = __builtin_amdgcn_readfirstlane(e.x >> 16);
+        c.h = __builtin_amdgcn_readfirstlane(e.x & 0xffff);
+        c.c0 = __builtin_amdgcn_readfirstlane(e.y);
+        c.bos = __builtin_amdgcn_readfirstlane(e.z);
+        c.eos = __builtin_amdgcn_readfirstlane(e.w);
+        c.nch = (c.eos - c.bos + BT - 1) / BT;
+    };
+    auto cur_init = [&](Cur &c) {
+        c.base = 0;
+        cur_load(c, 0);
+    };
+    // local chunk of virtual chunk J (clamped to the stream's last), moving c
+    // forward (the calls at one site never go back)
+    auto cur_seek = [&](Cur &c, int J) {
+        J = J < j1 ? J : j1 - 1;
+        while (J >= c.base + c.nch && c.k + 1 < KT) {
+            c.base += c.nch;
+            cur_load(c, c.k + 1);
+        }
+        return J - c.base;
+    };
+    // record of virtual chunk J (chunk c's record is in slot c: one pass)
+    auto cur_rec = [&](Cur &c, int J) {
+        const int j = cur_seek(c, J);
+        return ws + LY.recs + (static_cast<size_t>(c.c0 + j) * H + c.h) * kRecBytes;
+    };
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     // wave index as a scalar: the role branches below must be wave-uniform,
@@ -1456,21 +1631,32 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
 
     if (w < 4) {
         // ------------------------------- chain waves -------------------------------
-        int slot = a.state_indices[n];
-        if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
-            slot = 0;
-        }
+        // pool slot, tracked slot and length of sequence n, head h (PERS: of
+        // the item being scanned)
+        int slot = 0;
         int track_slot = 0;
         int track_len = -1;
-        if (a.track_indices != nullptr) {
-            track_slot = a.track_indices[n];
-            if (track_slot <= 0 || static_cast<int64_t>(track_slot) >= a.num_slots) {
-                track_slot = 0;
-            } else {
-                track_len = a.track_lens[n];
+        int64_t head_off = 0;
+        auto item_ctx = [&]() {
+            slot = a.state_indices[n];
+            if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
+                slot = 0;
             }
+            track_slot = 0;
+            track_len = -1;
+            if (a.track_indices != nullptr) {
+                track_slot = a.track_indices[n];
+                if (track_slot <= 0 || static_cast<int64_t>(track_slot) >= a.num_slots) {
+                    track_slot = 0;
+                } else {
+                    track_len = a.track_lens[n];
+                }
+            }
+            head_off = static_cast<int64_t>(h) * a.state_stride_head;
+        };
+        if constexpr (!PERS) {
+            item_ctx();
         }
-        const int64_t head_off = static_cast<int64_t>(h) * a.state_stride_head;
         // S rows [32wr, 32wr+32): tiles (kt = 2wr + tt, ct), lane holds
         // S[16kt + 4gq + i][col0 + 16ct + r]; the same element of slot s, and
         // of the carry buffer between segments
@@ -1486,7 +1672,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct) {
-                if (AFF && role > 0) {
+                if (PERS) {
+                    S[tt][ct] = z4;  // set per item below
+                } else if (AFF && role > 0) {
                     // zero, or the identity's columns col0 + 16ct + r
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -1549,7 +1737,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             }
         };
-        if (track_slot > 0 && track_len == 0 && first) {
+        if (!PERS && track_slot > 0 && track_len == 0 && first) {
             store_S(track_slot, S);
         }
         const char *tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
@@ -1584,8 +1772,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             float4 kesc;
             float vmax, kel1;
         };
-        auto read_b = [&](OpsB &op, int j) {
-            const char *st = sm.stg[j & 1];
+        auto read_b = [&](OpsB &op, int p) {
+            const char *st = sm.stg[p];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
             if constexpr (!LEAN) {
 #pragma unroll
@@ -1608,13 +1796,13 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                     op.vv[ct][i] = __uint_as_float(static_cast<uint32_t>(static_cast<uint16_t>(x[i])) << 16);
                 }
             }
-            const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[j & 1][0]);
+            const float4 um = *reinterpret_cast<const float4 *>(&sm.vmax[p][0]);
             op.vmax = max4_mag(um);
             op.kesc = *reinterpret_cast<const float4 *>(sc + kScKe + 4 * wr);
             op.kel1 = kel1_bound(sc);
         };
-        auto step = [&](int j, const OpsG &og, OpsG &next) {
-            const int p = j & 1;
+        // chunk j (of the item, PERS) in the stage of parity p
+        auto step = [&](int j, int p, const OpsG &og, OpsG &next) {
             const int len = eos - (bos + BT * j) < BT ? eos - (bos + BT * j) : BT;
             const char *st = sm.stg[p];
             const float *sc = reinterpret_cast<const float *>(st + St::kMisc) + DK;
@@ -1657,7 +1845,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             }
             lds_barrier();  // B1(j)
             OpsB ob;
-            read_b(ob, j);
+            read_b(ob, p);
             // B. y rows [16wr, 16wr+16) = v - (e^G k) S_j (one product per
             // slice, then scaled), published as fp16 hi/lo scaled by 2^sv;
             // tile wr is half wr%2 of slice wr/2. Phase C's operands of chunk
@@ -1777,43 +1965,163 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 load_g(gA, j0);
             }
         }
-        lds_barrier();  // B0: the first chunk's stage is written
-        if constexpr (LEAN) {
-            // chunk c's matrix operands are in gA when c - j0 is even, else gB
-            for (int j = j0; j < j1; j += 2) {
-                step(j, gA, gB);
-                if (j + 1 >= j1) {
+        if constexpr (PERS) {
+            Cur cc;  // the item being scanned
+            Cur cn;  // the next one, whose initial state is in Sn
+            f32x4 Sn[2][NT];
+            bool sn_zero = false;  // the next item has no state: Sn is a dummy load
+            // the chain's context of item c: sequence, head, tokens, and the
+            // slots from the table (no global loads at an item change)
+            auto enter = [&](const Cur &c) {
+                n = c.n;
+                h = c.h;
+                bos = c.bos;
+                eos = c.eos;
+                const int4 e = items[c.k][1];
+                slot = __builtin_amdgcn_readfirstlane(e.x);
+                track_slot = __builtin_amdgcn_readfirstlane(e.y);
+                track_len = __builtin_amdgcn_readfirstlane(e.z);
+                head_off = static_cast<int64_t>(h) * a.state_stride_head;
+                tr = ws + LY.tracks + (static_cast<size_t>(n) * H + h) * kTrBytes;
+            };
+            // the next item's initial state, loaded a whole item ahead. The
+            // loads are unconditional (an item without state reads the record
+            // area instead and is zeroed where Sn is used), so they go straight
+            // into Sn and are waited for only at the item change.
+            auto prefetch = [&]() {
+                if (cc.k + 1 < KT) {
+                    cn.base = cc.base + cc.nch;
+                    cur_load(cn, cc.k + 1);
+                    const int ns = __builtin_amdgcn_readfirstlane(items[cn.k][1].x);
+                    sn_zero = ns == 0;
+                    const float *src = sn_zero ? reinterpret_cast<const float *>(ws + LY.recs)
+                                               : a.state + ns * a.state_stride_slot +
+                                                     static_cast<int64_t>(cn.h) * a.state_stride_head;
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                        for (int ct = 0; ct < NT; ++ct) {
+                            const float4 s4 = load4(src + static_cast<int64_t>(col0 + 16 * ct + r) * DK +
+                                                    16 * (2 * wr + tt) + 4 * gq);
+                            Sn[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
+                        }
+                    }
+                }
+            };
+            if (j1 > 0) {
+                cur_init(cc);
+                enter(cc);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                    for (int ct = 0; ct < NT; ++ct) {
+                        if (slot > 0) {
+                            const float4 s4 = load4(state_ptr(slot, tt, ct));
+                            S[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
+                        } else {
+                            S[tt][ct] = z4;
+                        }
+                    }
+                }
+                if (track_slot > 0 && track_len == 0) {
+                    store_S(track_slot, S);
+                }
+                // the first item's state is waited for here, so the loop's
+                // steps do not wait for the prefetch behind it (that wait is
+                // at the item change, where Sn is used)
+                __builtin_amdgcn_s_waitcnt(kWaitVm0);
+                prefetch();
+            }
+            lds_barrier();  // B0: the first chunk's stage is written
+            // the stream: item after item, J the virtual chunk (every item has
+            // at least one chunk; the loop ends after KT items)
+            for (int J = 0; J < j1;) {
+                for (int j = 0; j < cc.nch; ++j, ++J) {
+                    step(j, J & 1, gA, gA);
+                }
+                if (slot > 0) {
+                    store_S(slot, S);
+                }
+                if (cc.k + 1 >= KT) {
                     break;
                 }
-                step(j + 1, gB, gA);
+                cc = cn;
+                enter(cc);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                    for (int ct = 0; ct < NT; ++ct) {
+                        S[tt][ct] = sn_zero ? z4 : Sn[tt][ct];
+                    }
+                }
+                if (track_slot > 0 && track_len == 0) {
+                    store_S(track_slot, S);
+                }
+                prefetch();
+            }
+            if (j1 > 0) {
+                lds_barrier();  // B1(j1)
+            }
+            // empty items keep their state; a tracked length of 0 copies it
+            for (int k = KT; k < KA; ++k) {
+                Cur ce;
+                cur_load(ce, k);
+                enter(ce);
+                if (track_slot > 0 && track_len == 0) {
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                        for (int ct = 0; ct < NT; ++ct) {
+                            if (slot > 0) {
+                                const float4 s4 = load4(state_ptr(slot, tt, ct));
+                                S[tt][ct] = f32x4{s4.x, s4.y, s4.z, s4.w};
+                            } else {
+                                S[tt][ct] = z4;
+                            }
+                        }
+                    }
+                    store_S(track_slot, S);
+                }
             }
         } else {
-            for (int j = j0; j < j1; ++j) {
-                step(j, gA, gA);
-            }
-        }
-        if (j1 > j0) {
-            lds_barrier();  // B1(j1)
-        }
-        if (AFF && fin_state != nullptr) {
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int ct = 0; ct < NT; ++ct) {
-                    put_aff(fin_state, tt, ct, S[tt][ct]);
+            lds_barrier();  // B0: the first chunk's stage is written
+            if constexpr (LEAN) {
+                // chunk c's matrix operands are in gA when c - j0 is even, else gB
+                for (int j = j0; j < j1; j += 2) {
+                    step(j, j & 1, gA, gB);
+                    if (j + 1 >= j1) {
+                        break;
+                    }
+                    step(j + 1, (j + 1) & 1, gB, gA);
+                }
+            } else {
+                for (int j = j0; j < j1; ++j) {
+                    step(j, j & 1, gA, gA);
                 }
             }
-        } else if (!last) {
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int ct = 0; ct < NT; ++ct) {
-                    *reinterpret_cast<float4 *>(carry_ptr(tt, ct)) =
-                        make_float4(S[tt][ct][0], S[tt][ct][1], S[tt][ct][2], S[tt][ct][3]);
-                }
+            if (j1 > j0) {
+                lds_barrier();  // B1(j1)
             }
-        } else if (slot > 0) {
-            store_S(slot, S);
+            if (AFF && fin_state != nullptr) {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                    for (int ct = 0; ct < NT; ++ct) {
+                        put_aff(fin_state, tt, ct, S[tt][ct]);
+                    }
+                }
+            } else if (!last) {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                    for (int ct = 0; ct < NT; ++ct) {
+                        *reinterpret_cast<float4 *>(carry_ptr(tt, ct)) =
+                            make_float4(S[tt][ct][0], S[tt][ct][1], S[tt][ct][2], S[tt][ct][3]);
+                    }
+                }
+            } else if (slot > 0) {
+                store_S(slot, S);
+            }
         }
     } else if (w < 8) {
         // ------------------------------- output waves ------------------------------
@@ -1837,8 +2145,14 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             f16x8 Aq[2];
             float4 qsc;
         };
+        Cur cl;  // PERS: load_out's position (one chunk ahead)
+        Cur co;  // PERS: finish's position (one chunk behind)
+        if (PERS && j1 > 0) {
+            cur_init(cl);
+            cur_init(co);
+        }
         auto load_out = [&](OpsO &op, int j) {
-            const char *rec = rec_of(j < j1 ? j : j1 - 1);
+            const char *rec = PERS ? cur_rec(cl, j) : rec_of(j < j1 ? j : j1 - 1);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 op.Qg[s] = as_f16x8(reinterpret_cast<const u32x4 *>(rec + kOffQg)[(wr * 4 + s) * 64 + lane]);
@@ -1903,13 +2217,23 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                     ot[(4 * gq + i) * CW + 16 * ct + r] = f32_to_bf16(acc[i]);
                 }
             }
-            const int t0 = bos + BT * j;
-            const int len = eos - t0 < BT ? eos - t0 : BT;
+            int jo = j;
+            int ob = bos;
+            int oe = eos;
+            int oh = h;
+            if constexpr (PERS) {
+                jo = cur_seek(co, j);
+                ob = co.bos;
+                oe = co.eos;
+                oh = co.h;
+            }
+            const int t0 = ob + BT * jo;
+            const int len = oe - t0 < BT ? oe - t0 : BT;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             const int row = lane >> 2;
             const int cq = lane & 3;
             const int t = 16 * wr + row;
-            uint16_t *dst = out + (static_cast<int64_t>(t0 + t) * H + h) * DK + col0 + cq * (CW / 4);
+            uint16_t *dst = out + (static_cast<int64_t>(t0 + t) * H + oh) * DK + col0 + cq * (CW / 4);
             if constexpr (NT == 1) {
                 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
                 const u32x2 val = *reinterpret_cast<const u32x2 *>(&sm.otile[wr][row][2 * cq]);
@@ -2024,8 +2348,16 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         // last row and are zeroed
         auto vrow = [&](int k) { return 16 * wl + k * (16 / NT) + lane / (4 * NT); };
         auto vcol = [&]() { return 4 * (lane % (4 * NT)); };
+        Cur cf;  // PERS: fetch's position (two chunks ahead)
+        Cur cv;  // PERS: fetch_v's (three ahead)
+        Cur cw;  // PERS: touch's (kWarmAhead ahead)
+        if (PERS && j1 > 0) {
+            cur_init(cf);
+            cur_init(cv);
+            cur_init(cw);
+        }
         auto fetch = [&](u32x4 (&R)[kPer], int j) {
-            const char *rec = rec_of(j < j1 ? j : j1 - 1);
+            const char *rec = PERS ? cur_rec(cf, j) : rec_of(j < j1 ? j : j1 - 1);
 #pragma unroll
             for (int k = 0; k < kPer; ++k) {
                 R[k] = reinterpret_cast<const u32x4 *>(rec + St::src(frag_of(k)))[lane];
@@ -2039,14 +2371,23 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
                 return;
             }
-            const int jc = j < j1 ? j : j1 - 1;
-            const int t0 = bos + BT * jc;
-            const int len = eos - t0 < BT ? eos - t0 : BT;
+            int jc = j < j1 ? j : j1 - 1;
+            int vb = bos;
+            int ve = eos;
+            int vh = h;
+            if constexpr (PERS) {
+                jc = cur_seek(cv, j);
+                vb = cv.bos;
+                ve = cv.eos;
+                vh = cv.h;
+            }
+            const int t0 = vb + BT * jc;
+            const int len = ve - t0 < BT ? ve - t0 : BT;
 #pragma unroll
             for (int k = 0; k < NT; ++k) {
                 const int row = vrow(k);
                 const int tc = row < len ? row : len - 1;
-                V[k] = *reinterpret_cast<const uint2 *>(vp + (static_cast<int64_t>(t0 + tc) * H + h) * DK + col0 +
+                V[k] = *reinterpret_cast<const uint2 *>(vp + (static_cast<int64_t>(t0 + tc) * H + vh) * DK + col0 +
                                                         vcol());
                 const uint32_t keep = keep_mask(row < len);
                 V[k].x &= keep;
@@ -2086,7 +2427,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             wb[k] = 0;
         }
         auto touch = [&](uint32_t (&dst)[kTouch], int jj) {
-            const char *rec = rec_of(jj < j1 ? jj : j1 - 1);
+            const char *rec = PERS ? cur_rec(cw, jj) : rec_of(jj < j1 ? jj : j1 - 1);
 #pragma unroll
             for (int k = 0; k < kTouch; ++k) {
                 warm ^= dst[k];
@@ -2153,21 +2494,40 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     }
 
     // Tokens outside every sequence are written as zero.
-    auto zero_rows = [&](int ta, int tb) {
+    auto zero_rows = [&](int ta, int tb, int hh) {
         for (int t = ta + tid / 16; t < tb; t += kScanThreads / 16) {
             if ((tid & 15) == 0) {
                 // one thread per token row writes this group's CW columns
                 for (int cidx = 0; cidx < CW; ++cidx) {
-                    out[(static_cast<int64_t>(t) * H + h) * DK + col0 + cidx] = 0;
+                    out[(static_cast<int64_t>(t) * H + hh) * DK + col0 + cidx] = 0;
                 }
             }
         }
     };
-    if (n == 0 && first) {
-        zero_rows(0, bos);
-    }
-    if (n == N - 1 && (last || zero_outside)) {
-        zero_rows(eos, a.num_tokens);
+    if constexpr (PERS) {
+        // the team's items of sequences 0 and N - 1 (bits set with the table)
+        for (int word = 0; word < (KA + 31) / 32; ++word) {
+            uint32_t bits = edge_items[word];
+            while (bits != 0u) {
+                const int k = 32 * word + __builtin_ctz(bits);
+                bits &= bits - 1u;
+                Cur ce;
+                cur_load(ce, k);
+                if (ce.n == 0) {
+                    zero_rows(0, ce.bos, ce.h);
+                }
+                if (ce.n == N - 1) {
+                    zero_rows(ce.eos, a.num_tokens, ce.h);
+                }
+            }
+        }
+    } else {
+        if (n == 0 && first) {
+            zero_rows(0, bos, h);
+        }
+        if (n == N - 1 && (last || zero_outside)) {
+            zero_rows(eos, a.num_tokens, h);
+        }
     }
 }
 
@@ -2724,10 +3084,20 @@ int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, int ring, int win, b
     if (static_cast<int64_t>(nrec) * a.num_heads > 0x7fffffff || blocks > 0x7fffffff) {
         return KDA_ERR_INVALID_ARGUMENT;
     }
+    // The persistent scan (see chunk_scan_kernel): one pass over several
+    // sequences with 32-column groups and more (sequence, head) items than
+    // teams of workgroups, one workgroup per CU, at most kPersMaxItems items
+    // per team.
+    const int group = 8 * (8 / nt);
+    const int64_t teams = device_cus(st) / group * 8;
+    const bool pers = win <= 0 && nt == 2 && a.num_seqs > 1 && a.num_seqs <= kPersMaxSeqs && teams > 0 &&
+                      pairs > teams && pairs <= kPersMaxItems * teams;
     if (a.num_seqs > 1) {  // one sequence needs no chunk index (K1 and K2 derive it)
         const Layout LY = layout(a.num_tokens, a.num_seqs, a.num_heads, ring);
         int *cs = reinterpret_cast<int *>(ws + LY.chunk_start);
-        void *params[] = {&kargs, &cs};
+        int4 *sched = reinterpret_cast<int4 *>(ws + LY.sched);
+        int sort = pers ? 1 : 0;
+        void *params[] = {&kargs, &cs, &sched, &sort};
         if (hipLaunchKernel(reinterpret_cast<const void *>(chunk_index_kernel), dim3(1), dim3(1024),
                             params, 0, st) != hipSuccess) {
             return KDA_ERR_LAUNCH;
@@ -2755,6 +3125,17 @@ int launch(const KdaChunkArgs &a, char *ws, hipStream_t st, int ring, int win, b
                                params, 0, st) == hipSuccess;
     };
     if (win <= 0) {
+        if (pers) {
+            const char *cws = ws;
+            int rg = ring, l = 0, h = 0;
+            void *params[] = {&kargs, &cws, &rg, &l, &h};
+            return launch_prep(0, nrec, st) &&
+                           hipLaunchKernel(reinterpret_cast<const void *>(chunk_scan_kernel<2, false, false, true>),
+                                           dim3(static_cast<unsigned>(teams * (8 / nt))), dim3(kScanThreads), params,
+                                           0, st) == hipSuccess
+                       ? KDA_OK
+                       : KDA_ERR_LAUNCH;
+        }
         return launch_prep(0, nrec, st) && launch_scan(false, 0, 0) ? KDA_OK : KDA_ERR_LAUNCH;
     }
     // one sequence; segments cover the chunks T tokens can hold (a shorter

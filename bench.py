@@ -19,7 +19,8 @@ Also reported in the same JSON line:
   measured on is unchanged (``source_sha256`` in the summary); ``copy_gbs`` is
   what a plain 512 MiB device-to-device copy reaches on the same GPU (bytes read
   plus written per time), a reference for the achievable streaming rate;
-* ``more_configs`` -- configs 4 and 5 (prefill) and config 5's 4-token decode;
+* ``more_configs`` -- configs 4 and 5 (prefill), a serving-shaped batch of 64
+  prompts x 256 tokens on 32 heads (prefill), and config 5's 4-token decode;
 * ``latency_rows`` -- the reference bench's deployed shapes
   (bench/kda_recurrent/bench_kda_varlen_recurrent.py:81-114,534-551): decode
   H16/32/64 x B1/32/128, the five checkpointed verify shapes, recurrent
@@ -296,7 +297,8 @@ def _device_case(heads, lengths, *, slots, indices, seed, gate=(1.0, 0.0), zero_
 
 
 def run_more(steps, warmup):
-    """Configs 4 and 5 prefill, and config 5's 4-token decode, on the device."""
+    """Configs 4 and 5 prefill, a batch of 64 short prompts, and config 5's
+    4-token decode, on the device."""
     from tests import kda_cases as C
 
     ops = torch.ops.sgl_glm53_ascend
@@ -333,6 +335,9 @@ def run_more(steps, warmup):
     idx4 = torch.randperm(64, generator=g4)[:16].tolist()
     prefill("config4_prefill", 32, lengths4, 64, idx4, 4, (1.0, 0.0), False)
     prefill("config5_prefill", 16, [65536], 2, [1], 5, (2.0, -2.0), True)
+    # a serving-shaped batch: 64 prompts x 256 tokens (2048 (sequence, head)
+    # items, which the scan runs on persistent workgroups)
+    prefill("batch64x256_prefill", 32, [256] * 64, 65, list(range(1, 65)), 6, (1.0, 0.0), False)
 
     # config 5 decode: 1024 sequences x 4 tokens from a 2048-slot pool, harsh decay
     n5, steps5, h5, slots5 = 1024, 4, 16, 2048

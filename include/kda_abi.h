@@ -212,7 +212,10 @@ size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
  * sequence on few heads that takes the affine form scans its P segments at
  * once (segment s > 0 from zero and from the identity) and combines them
  * (S_{s+1} = Phi_s S_s + Z_s, outputs corrected by O_t S_s), all on
- * `stream`.
+ * `stream`. Several sequences with more (sequence, head) pairs than the
+ * device's CUs / 4 run their scan on one persistent workgroup per CU, each
+ * team of four taking several pairs, longest first (the chunk-index pass
+ * orders them); results are those of a workgroup per pair.
  * Alignment
  * (KDA_ERR_INVALID_ARGUMENT otherwise): state 16 bytes with strides in
  * multiples of 4 elements; q, k, v and out 8 bytes; gate 8 (RAW) or 16. */

@@ -146,7 +146,8 @@ def test_chunk_launch_alignment_checks_need_no_device(lib):
 
 def test_chunk_workspace_size_formula(lib):
     """kda_chunk_workspace_bytes is a host-only function of (T, N, H, D): the
-    chunk-start table, 55 KiB records, one 16.75 KiB tracking record per
+    chunk-start table (and for several sequences the schedule table that
+    orders them for the persistent scan), 55 KiB records, one 16.75 KiB tracking record per
     (sequence, head) and, for a single sequence, one 64 KiB state per head
     carried between scan segments, each 256-byte aligned (the sizes the
     integration notes quote for sizing a reusable workspace). The records: one
@@ -171,6 +172,8 @@ def test_chunk_workspace_size_formula(lib):
 
     def classic(T, N, H):
         header = ((N + 1) * 4 + 255) // 256 * 256
+        if N > 1:  # the schedule table of several sequences: 2N + 1 int4
+            header += ((2 * N + 1) * 16 + 255) // 256 * 256
         chunks = (T + 63) // 64
         slots = chunks + N
         if N == 1 and T >= 16384 and H <= 16:

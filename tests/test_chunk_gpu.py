@@ -284,6 +284,53 @@ def test_prepared_chunk_many_sequences(gpu_ops):
     assert torch.equal(pool.cpu()[other], case.pool[other]), "an unused slot was written"
 
 
+@pytest.mark.parametrize("heads", [1, 2])
+def test_chunk_persistent_scan_tracking_and_padding(gpu_ops, heads):
+    """More (sequence, head) items than the scan has teams of workgroups (64 on
+    a 256-CU device), so persistent workgroups take several items each,
+    longest first, and stage an item's first chunks while the previous one
+    finishes: ragged and empty sequences, the padding slot, tracked prefixes
+    at 0, inside a chunk, on a chunk boundary and at the end (also of empty
+    sequences), and tokens before the first and after the last sequence --
+    against the oracle; unindexed slots byte-identical."""
+    import random
+
+    rng = random.Random(11 + heads)
+    n = 160 // heads + 7
+    lengths = [rng.choice([0, 1, 16, 17, 63, 64, 65, 128, 130, 200]) for _ in range(n)]
+    indices = [0 if rng.random() < 0.08 else s for s in range(1, n + 1)]
+    track_idx, track_lens = [], []
+    for i, length in enumerate(lengths):
+        if i % 4 == 1:
+            track_idx.append(n + 1 + i)
+            track_lens.append(rng.choice([0, length, rng.randint(0, length), length // 64 * 64]))
+        else:
+            track_idx.append(0)
+            track_lens.append(0)
+    slots = 2 * n + 2
+    # two dummy sequences frame the real ones: their tokens lie outside every
+    # sequence once they are dropped from cu_seqlens
+    case = C.raw_case(heads, [3] + lengths + [5], indices=[0] + indices + [0], slots=slots,
+                      seed=4000 + heads, track=([0] + track_idx + [0], [0] + track_lens + [0]))
+    case.cu_seqlens = case.cu_seqlens[1:-1].clone()
+    case.indices = case.indices[1:-1].clone()
+    case.track_indices = case.track_indices[1:-1].clone()
+    case.track_lens = case.track_lens[1:-1].clone()
+    assert len(case.indices) * heads > 64
+    out, pool = _run_chunk(gpu_ops, case)
+    ref_pool = C.clone_pool(case.pool)
+    ref = _oracle_chunk(case, ref_pool)
+    out = out.cpu()
+    T = case.q.shape[1]
+    assert torch.equal(out[0, :3], torch.zeros_like(out[0, :3]))
+    assert torch.equal(out[0, T - 5:], torch.zeros_like(out[0, T - 5:]))
+    C.assert_out(out, ref, C.OUT_TOL, "output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
+    touched = set(s for s in indices if s > 0) | set(s for s in track_idx if s > 0)
+    other = [s for s in range(slots) if s not in touched]
+    assert torch.equal(pool.cpu()[other], case.pool[other]), "an unindexed slot was written"
+
+
 @pytest.mark.parametrize(
     "name,heads,lengths,slots,indices,gate",
     [
