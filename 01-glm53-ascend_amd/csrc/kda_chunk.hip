@@ -385,10 +385,18 @@ constexpr int kPersMaxSeqs = 4096;
 constexpr int kPersMaxItems = 256;
 
 __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a, int *cs, int4 *sched, int sort) {
-    __shared__ int part[1024];
-    __shared__ unsigned long long key[kPersMaxSeqs];
+    // With the schedule, every per-sequence value is loaded once, up front,
+    // into LDS, so the sort and the table wait on no global round trip.
+    __shared__ int part[16];                            // each wave's chunk total
+    __shared__ unsigned long long key[kPersMaxSeqs];    // (chunks + 1, ~n)
+    __shared__ int4 info[kPersMaxSeqs];                 // (bos, eos, chunk start, pool slot)
+    __shared__ int2 tinfo[kPersMaxSeqs];                // (tracked slot, tracked length)
     const int N = a.num_seqs;
+    const bool dosort = sort != 0 && N <= kPersMaxSeqs;
+    const bool track = a.track_indices != nullptr;
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const int per = (N + 1023) / 1024;
     const int begin = tid * per;
     const int end = begin + per < N ? begin + per : N;
@@ -396,46 +404,114 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
     for (int n = begin; n < end; ++n) {
         int bos, eos;
         seq_bounds(a, n, bos, eos);
-        sum += (eos - bos + BT - 1) / BT;
+        const int c = (eos - bos + BT - 1) / BT;
+        sum += c;
+        if (dosort) {
+            int slot = a.state_indices[n];
+            if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
+                slot = 0;
+            }
+            int tslot = 0;
+            int tlen = -1;
+            if (track) {
+                tslot = a.track_indices[n];
+                const int tl = a.track_lens[n];
+                if (tslot <= 0 || static_cast<int64_t>(tslot) >= a.num_slots) {
+                    tslot = 0;
+                } else {
+                    tlen = tl;
+                }
+            }
+            info[n] = make_int4(bos, eos, 0, slot);
+            tinfo[n] = make_int2(tslot, tlen);
+            key[n] = (static_cast<unsigned long long>(c + 1) << 32) | (0xffffffffu - static_cast<unsigned>(n));
+        }
     }
-    part[tid] = sum;
+    // exclusive prefix of the per-thread sums: within the wave by lane
+    // shuffles, across the 16 waves through LDS
+    int inc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(inc, off);
+        inc += lane >= off ? o : 0;
+    }
+    if (lane == 63) {
+        part[wave] = inc;
+    }
     __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int add = tid >= off ? part[tid - off] : 0;
-        __syncthreads();
-        part[tid] += add;
-        __syncthreads();
+    int run = inc - sum;
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const int p = part[w];
+        run += w < wave ? p : 0;
+        total += p;
     }
-    int run = tid == 0 ? 0 : part[tid - 1];
     for (int n = begin; n < end; ++n) {
         cs[n] = run;
         int bos, eos;
-        seq_bounds(a, n, bos, eos);
+        if (dosort) {
+            const int4 in = info[n];
+            info[n].z = run;
+            bos = in.x;
+            eos = in.y;
+        } else {
+            seq_bounds(a, n, bos, eos);
+        }
         run += (eos - bos + BT - 1) / BT;
     }
     if (tid == 1023) {
-        cs[N] = part[1023];
+        cs[N] = total;
     }
-    if (sort == 0 || N > kPersMaxSeqs) {
+    if (!dosort) {
         return;
     }
-    // bitonic sort, descending, of (chunks + 1, ~n): padding (zero) sorts
-    // after every sequence, empty ones included
+    // Sort descending by (chunks + 1, ~n): padding (zero) sorts after every
+    // sequence, empty ones included. Up to 64 sequences: one wave, bitonic
+    // through lane exchanges; beyond, bitonic in LDS.
     int npad = 1;
     while (npad < N) {
         npad <<= 1;
     }
-    for (int i = tid; i < npad; i += 1024) {
-        unsigned long long kk = 0;
-        if (i < N) {
-            int bos, eos;
-            seq_bounds(a, i, bos, eos);
-            const unsigned c = static_cast<unsigned>((eos - bos + BT - 1) / BT);
-            kk = (static_cast<unsigned long long>(c + 1) << 32) | (0xffffffffu - static_cast<unsigned>(i));
+    if (npad <= 64) {
+        __syncthreads();  // info, tinfo and key complete
+        if (wave != 0) {
+            return;
         }
-        key[i] = kk;
+        unsigned long long x = lane < N ? key[lane] : 0ull;
+#pragma unroll
+        for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const unsigned lo = __shfl_xor(static_cast<unsigned>(x), stride);
+                const unsigned hi = __shfl_xor(static_cast<unsigned>(x >> 32), stride);
+                const unsigned long long y = (static_cast<unsigned long long>(hi) << 32) | lo;
+                const bool lower = (lane & stride) == 0;
+                const bool desc = (lane & size) == 0;
+                x = lower == desc ? (x > y ? x : y) : (x < y ? x : y);
+            }
+        }
+        const unsigned nlo = __shfl_down(static_cast<unsigned>(x), 1);
+        const unsigned nhi = __shfl_down(static_cast<unsigned>(x >> 32), 1);
+        const unsigned long long xn = (static_cast<unsigned long long>(nhi) << 32) | nlo;
+        if (lane < N) {
+            const int n = static_cast<int>(0xffffffffu - static_cast<unsigned>(x & 0xffffffffu));
+            const int4 in = info[n];
+            const int2 ti = tinfo[n];
+            sched[2 * lane] = make_int4(n, in.z, in.x, in.y);
+            sched[2 * lane + 1] = make_int4(in.w, ti.x, ti.y, 0);
+            const bool nonempty = (x >> 32) > 1;
+            const bool next_empty = lane + 1 == N || (xn >> 32) <= 1;
+            if ((nonempty && next_empty) || (lane == 0 && !nonempty)) {
+                sched[2 * N] = make_int4(nonempty ? lane + 1 : 0, 0, 0, 0);
+            }
+        }
+        return;
     }
-    __syncthreads();  // also orders every thread's chunk_start stores before the reads below
+    for (int i = N + tid; i < npad; i += 1024) {
+        key[i] = 0ull;
+    }
+    __syncthreads();
     for (int size = 2; size <= npad; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             for (int i = tid; i < npad; i += 1024) {
@@ -454,26 +530,13 @@ __global__ __launch_bounds__(1024) void chunk_index_kernel(const KdaChunkArgs a,
         }
     }
     for (int r = tid; r < N; r += 1024) {
-        const int n = static_cast<int>(0xffffffffu - static_cast<unsigned>(key[r] & 0xffffffffu));
-        int bos, eos;
-        seq_bounds(a, n, bos, eos);
-        int slot = a.state_indices[n];
-        if (slot < 0 || static_cast<int64_t>(slot) >= a.num_slots) {
-            slot = 0;
-        }
-        int tslot = 0;
-        int tlen = -1;
-        if (a.track_indices != nullptr) {
-            tslot = a.track_indices[n];
-            if (tslot <= 0 || static_cast<int64_t>(tslot) >= a.num_slots) {
-                tslot = 0;
-            } else {
-                tlen = a.track_lens[n];
-            }
-        }
-        sched[2 * r] = make_int4(n, cs[n], bos, eos);
-        sched[2 * r + 1] = make_int4(slot, tslot, tlen, 0);
-        const bool nonempty = (key[r] >> 32) > 1;
+        const unsigned long long x = key[r];
+        const int n = static_cast<int>(0xffffffffu - static_cast<unsigned>(x & 0xffffffffu));
+        const int4 in = info[n];
+        const int2 ti = tinfo[n];
+        sched[2 * r] = make_int4(n, in.z, in.x, in.y);
+        sched[2 * r + 1] = make_int4(in.w, ti.x, ti.y, 0);
+        const bool nonempty = (x >> 32) > 1;
         const bool next_empty = r + 1 == N || (key[r + 1] >> 32) <= 1;
         if ((nonempty && next_empty) || (r == 0 && !nonempty)) {
             sched[2 * N] = make_int4(nonempty ? r + 1 : 0, 0, 0, 0);

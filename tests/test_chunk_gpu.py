@@ -284,12 +284,13 @@ def test_prepared_chunk_many_sequences(gpu_ops):
     assert torch.equal(pool.cpu()[other], case.pool[other]), "an unused slot was written"
 
 
-@pytest.mark.parametrize("heads", [1, 2])
+@pytest.mark.parametrize("heads", [1, 2, 4])
 def test_chunk_persistent_scan_tracking_and_padding(gpu_ops, heads):
     """More (sequence, head) items than the scan has teams of workgroups (64 on
     a 256-CU device), so persistent workgroups take several items each,
     longest first, and stage an item's first chunks while the previous one
-    finishes: ragged and empty sequences, the padding slot, tracked prefixes
+    finishes (167, 87 and 47 sequences: the schedule is sorted in LDS, and
+    for 64 or fewer within one wave): ragged and empty sequences, the padding slot, tracked prefixes
     at 0, inside a chunk, on a chunk boundary and at the end (also of empty
     sequences), and tokens before the first and after the last sequence --
     against the oracle; unindexed slots byte-identical."""
