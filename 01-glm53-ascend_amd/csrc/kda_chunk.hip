@@ -562,9 +562,12 @@ constexpr int kPadX = 68;   // fp32 row stride of [64][64] tiles (16-B rows)
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Akk / Aqk exponent anchor: row 7 of each 16-row block, and the largest
-// exponent (log2 units) a factor may take before it is clamped.
+// exponent (log2 units) a factor may take before it is clamped. A chunk in
+// which some block's factors would span more than kExactExp2 (the margin
+// covers the rounding of the cumsum) takes the exact form instead.
 constexpr int kAnchorRow = 7;
 constexpr float kMaxExp2 = 126.f;
+constexpr float kExactExp2 = 125.f;
 
 // All-ones if `keep`, else zero, opaque to the optimizer: a value masked with
 // it is used unconditionally, so its load cannot be sunk into a branch (a
@@ -599,6 +602,7 @@ struct PrepShared {
     } u;
     float beta[BT];
     float gsum[4][DK];  // each wave's two row groups' decay sums (the cumsum's carries)
+    alignas(16) int far[4];  // per wave: some anchor factor of its rows spans > kExactExp2
 };
 static_assert(sizeof(PrepShared) <= 80 * 1024, "two prepare workgroups per CU");
 
@@ -811,6 +815,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             *reinterpret_cast<float4 *>(&sm.gsum[wave][4 * kc]) =
                 make_float4(other.x + run.x, other.y + run.y, other.z + run.z, other.w + run.w);
         }
+        // The anchor factors' largest exponents in this lane's rows: rows
+        // 16I .. 16I + 7 (even rg) end at the anchor, so e^(G_16I - anchor)
+        // is their row factor; rows 16I + 8 .. 16I + 15 (odd rg) start after
+        // it, so e^(anchor - G_16I+15) is their column factor (decays g <= 0)
+        {
+            const float4 d = odd ? make_float4(-run.x, -run.y, -run.z, -run.w)
+                                 : make_float4(gcum[0].x - run.x, gcum[0].y - run.y, gcum[0].z - run.z,
+                                               gcum[0].w - run.w);
+            const bool far = fmaxf(fmaxf(d.x, d.y), fmaxf(d.z, d.w)) > kExactExp2;
+            // every lane stores the wave's same value (no branch)
+            sm.far[wave] = __ballot(far) != 0ull;
+        }
         gprev = odd ? other : make_float4(0.f, 0.f, 0.f, 0.f);
         if (tid < BT) {
             float b = braw;
@@ -887,6 +903,49 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         x[5] = g1.y;
         x[6] = g1.z;
         x[7] = g1.w;
+    };
+
+    // The exact form of pair (I, J) over this wave's channel half, for a
+    // chunk whose anchor factors would be clamped: every element's own
+    // e^(G_i - G_j) (<= 1 for j <= i under decay; the entries above the
+    // diagonal, which nothing reads, are clamped), in fp32. For each row x
+    // of the block, lane (r, gq) sums its 16 channels of Akk[16I + x][16J + r]
+    // and Aqk[16I + r][16J + x]; the four lanes of each r add their channels,
+    // and the lane whose MFMA layout holds the entry keeps it.
+    auto exact_pair = [&](int I, int J, int ri, const float (&qv)[2][8], float qscale, f32x4 &akk, f32x4 &aqt) {
+#pragma unroll 1
+        for (int x = 0; x < 16; ++x) {
+            float a = 0.f, b = 0.f;
+#pragma unroll 1
+            for (int sl = 0; sl < 2; ++sl) {
+                const int s = 2 * sh + sl;
+                float kj[8], gj[8], gi[8], kx[8], gx[8], ky[8], gy[8];
+                load_k8(16 * J + r, s, kj);
+                load_g8(16 * J + r, s, gj);
+                load_g8(ri, s, gi);
+                load_k8(16 * I + x, s, kx);
+                load_g8(16 * I + x, s, gx);
+                load_k8(16 * J + x, s, ky);
+                load_g8(16 * J + x, s, gy);
+                const float *q = sl == 0 ? qv[0] : qv[1];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    a = fmaf(kx[e] * kj[e], ex2(fminf(gx[e] - gj[e], kMaxExp2)), a);
+                    b = fmaf(q[e] * ky[e], ex2(fminf(gi[e] - gy[e], kMaxExp2)), b);
+                }
+            }
+            a += __shfl_xor(a, 16);
+            a += __shfl_xor(a, 32);
+            b += __shfl_xor(b, 16);
+            b += __shfl_xor(b, 32);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (x == 4 * gq + e) {
+                    akk[e] = a;
+                    aqt[e] = b * qscale;
+                }
+            }
+        }
     };
 
     // ---- S3: Akk (-> L^T), Aqk (-> LT's lower triangle), q e^G fragments ----
@@ -997,7 +1056,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             pq[ii][J] = aqt;
         }
     }
-
     // ---- S4: kd fragments (kept for S6), e^(G_last), tracking operands, e^G k
     // fragments of the record --------------------------------------------------
     // k[t][16mk + r] for the rows t = 32s + kperm(gq, e) of a kd^T fragment:
@@ -1091,6 +1149,57 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             }
         }
     }
+    // A chunk beyond the anchors' span: S3's products were formed from
+    // clamped factors; the exact form replaces them here, behind S4 and
+    // before G and K die (the q rows reloaded, so nothing of S3 stays live
+    // for it). The flags are read only here: their wait would otherwise
+    // land on the cumsum's path.
+    const bool exact = __builtin_amdgcn_readfirstlane(sm.far[0] | sm.far[1] | sm.far[2] | sm.far[3]) != 0;
+    if (__builtin_expect(exact, 0)) {  // laid out after the kernel's straight-line path
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const int I = ii == 0 ? IA : 3 - IA;
+            const int ri = 16 * I + r;
+            int tc = ri < len ? ri : len - 1;
+            // opaque, so this address is formed here rather than shared with
+            // S1's q loads (whose registers would then stay live through S4)
+            asm volatile("" : "+v"(tc));
+            const uint16_t *row = qp + (static_cast<int64_t>(t0 + tc) * H + h) * DK;
+            const uint32_t keep = keep_mask(ri < len);
+            float qv[2][8];
+#pragma unroll
+            for (int q2 = 0; q2 < 2; ++q2) {
+                const int s = 2 * sh + q2;
+                const uint2 q0 = *reinterpret_cast<const uint2 *>(row + 32 * s + 4 * gq);
+                const uint2 q1 = *reinterpret_cast<const uint2 *>(row + 32 * s + 16 + 4 * gq);
+                const uint32_t w[4] = {q0.x & keep, q0.y & keep, q1.x & keep, q1.y & keep};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qv[q2][2 * e] = __uint_as_float(w[e] << 16);
+                    qv[q2][2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+                }
+            }
+            float qscale = a.scale;
+            if (norm) {
+                qscale = a.scale * __builtin_amdgcn_rsqf(sm.u.early.qss[0][ri] + sm.u.early.qss[1][ri] + 1e-6f);
+            }
+            const int nj = ii == 0 ? I + 1 : (I + 1 < 2 ? I + 1 : 2);
+#pragma unroll 1
+            for (int J = 0; J < nj; ++J) {
+                f32x4 akk = {0.f, 0.f, 0.f, 0.f};
+                f32x4 aqt = {0.f, 0.f, 0.f, 0.f};
+                exact_pair(I, J, ri, qv, qscale, akk, aqt);
+#pragma unroll
+                for (int Js = 0; Js < (ii == 0 ? 4 : 2); ++Js) {
+                    if (Js == J) {
+                        pk[ii][Js] = akk;
+                        pq[ii][Js] = aqt;
+                    }
+                }
+            }
+        }
+    }
+
     lds_barrier();  // G and K are dead from here on
     // S3's two channel halves meet in LT, which lies over the dead G: half
     // sh = 1 stores its partial products, then half sh = 0 adds its own and

@@ -155,10 +155,11 @@ at::Tensor run_chunk(const char *op, KdaChunkArgs &args, const at::Tensor &q);
 // runs in the chunked form (measured: 1024 tokens on 4 heads take ~1 ms
 // token by token, a few tens of microseconds in 64-token chunks).
 constexpr int64_t kChunkRouteTokensPerRequest = 128;
-// ... but only inside the chunk kernels' exponent envelope: with raw gates
+// ... but only inside the chunk kernels' anchored envelope: with raw gates
 // g >= lower_bound per token, so 8 tokens decay by at most 8 |lower_bound|
-// nat, which must stay below 2^126 (87.3 nat); a lower bound under this
-// keeps the token loop, which has no such limit.
+// nat, below 2^126 (87.3 nat). Beyond it the chunk kernels stay exact but
+// form every steep chunk's products element by element, so a lower bound
+// under this keeps the token loop.
 constexpr double kChunkRouteMinLowerBound = -10.9;
 // ... and with a bounded workspace: the token loop allocates nothing beyond
 // the output, so the chunked route takes at most this much scratch. A single

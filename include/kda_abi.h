@@ -192,13 +192,13 @@ size_t kda_chunk_workspace_bytes(int32_t num_tokens, int32_t num_seqs,
                                  int32_t num_heads, int32_t head_dim);
 
 /* Chunked (chunk = 64 tokens) KDA over packed varlen sequences.
- * Decay precondition: the intra-chunk products factor e^(G_i - G_j) as
- * e^(G_i - a) e^(a - G_j) with the anchor a at the middle of each 16-token
- * block, so no factor spans more than 8 tokens of decay. Results are exact
- * (to the tolerance contract) while any 8 consecutive tokens of a channel
- * decay by less than 2^126 (about 87 nat): always on the RAW path with
- * lower_bound >= -10.9, and for LOG gates g >= -10.9 per token. Beyond it
- * the exponents are clamped: outputs and states stay finite but inexact.
+ * Decays (g <= 0) of any magnitude: the intra-chunk products factor
+ * e^(G_i - G_j) as e^(G_i - a) e^(a - G_j) with the anchor a at the middle of
+ * each 16-token block, which holds while any 8 consecutive tokens of a
+ * channel decay by less than 2^125 (about 87 nat: always on the RAW path with
+ * lower_bound >= -10.9, and for LOG gates g >= -10.9 per token). A chunk
+ * with a steeper block forms those products element by element instead
+ * (exact, to the same tolerance contract, and slower for that chunk).
  * `workspace`
  * must be 256-byte aligned device memory of kda_chunk_workspace_bytes(...)
  * bytes; its contents need no initialization. A single sequence (N == 1)

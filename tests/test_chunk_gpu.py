@@ -242,18 +242,52 @@ def test_prepared_chunk_weak_decay(gpu_ops, heads, T):
     print(f"weak decay H{heads} T{T}: output err {e_o:.2e}, state err {e_s:.2e}")
 
 
-def test_prepared_chunk_beyond_envelope_stays_finite(gpu_ops):
-    """Per-token decays beyond the stated envelope (8 tokens at g = -20 span
-    160 nat) give finite outputs and states: the factor exponents are clamped
-    rather than overflowing to inf / NaN."""
+@pytest.mark.parametrize("form", ["all chunks", "bursts"])
+def test_prepared_chunk_beyond_envelope_exact(gpu_ops, form):
+    """Decays steeper than the anchored factors hold (8 tokens spanning more
+    than 2^125): such a chunk takes the exact form (per-element
+    e^(G_i - G_j)) and matches the fp64 oracle like any other. "all chunks":
+    g = -20 on every token (8 tokens span 160 nat). "bursts": ordinary gates
+    with g = -25 on 16 channels of tokens 70-89 and -40 on every channel of
+    tokens 200-203, so two chunks of the first sequence take the exact form
+    and the rest the anchored one, in one call."""
     import dataclasses
 
-    case = C.prepared_case(2, (128,), slots=2, indices=[1], seed=45)
-    case = dataclasses.replace(case, g=torch.full(tuple(case.g.shape), -20.0))
+    case = C.prepared_case(2, (300, 100), slots=4, indices=[1, 3], seed=45)
+    g = case.g.clone()
+    if form == "all chunks":
+        g.fill_(-20.0)
+    else:
+        g[:, 70:90, :, 0:16] = -25.0
+        g[:, 200:204] = -40.0
+    case = dataclasses.replace(case, g=g)
     dev = _prepared_dev(case)
     pool = C.to_dev(case.pool, DEV)
     out = _chunk_prepared(gpu_ops, case, pool, dev)
     assert torch.isfinite(out).all() and torch.isfinite(pool).all()
+    ref_pool = C.clone_pool(case.pool).double()
+    ref = R.kda_chunk(case.q.double() * case.scale, case.k.double(), case.v.double(),
+                      case.g.double(), case.beta.double(), state_pool=ref_pool,
+                      state_indices=case.indices, cu_seqlens=case.cu_seqlens,
+                      dtype=torch.float64, out_dtype=torch.float64)
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, f"{form} output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, f"{form} pool")
+
+
+def test_raw_chunk_beyond_envelope_exact_with_tracking(gpu_ops):
+    """The raw-gate chunk op below the router's bound (lower_bound = -15 with
+    the gate saturated, g ~ -14.7 per token: every chunk takes the exact
+    form), with prefixes tracked inside a chunk and on a chunk boundary,
+    against the oracle."""
+    case = C.raw_case(4, (200, 130), indices=[1, 2], slots=6, seed=1213, lower_bound=-15.0,
+                      track=([4, 5], [90, 64]))
+    case.a = (case.a.float() + 4.0).bfloat16()
+    out, pool = _run_chunk(gpu_ops, case)
+    assert torch.isfinite(out).all() and torch.isfinite(pool).all()
+    ref_pool = C.clone_pool(case.pool)
+    ref = _oracle_chunk(case, ref_pool)
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, "output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
 
 
 def test_prepared_chunk_many_sequences(gpu_ops):
