@@ -318,6 +318,34 @@ def test_prepared_chunk_many_sequences(gpu_ops):
     assert torch.equal(pool.cpu()[other], case.pool[other]), "an unused slot was written"
 
 
+@pytest.mark.parametrize("n,heads", [(5000, 1), (2100, 8)])
+def test_prepared_chunk_beyond_persistent_limits(gpu_ops, n, heads):
+    """Batches the persistent scan does not take, so the chunk-index pass
+    writes no schedule: more sequences than it sorts (5000 > 4096), and more
+    (sequence, head) items than 256 per team of 64 (2100 x 8 = 16800 >
+    16384). Short ragged and empty sequences against the oracle; unused slots
+    byte-identical."""
+    import random
+
+    rng = random.Random(n + heads)
+    lengths = [rng.choice([0, 1, 2, 64, 65]) if rng.random() < 0.2 else rng.randint(1, 40) for _ in range(n)]
+    slots = n + 8
+    indices = [0 if rng.random() < 0.03 else s for s in rng.sample(range(1, slots), n)]
+    case = C.prepared_case(heads, lengths, slots=slots, indices=indices, seed=n + 7 * heads)
+    dev = _prepared_dev(case)
+    pool = C.to_dev(case.pool, DEV)
+    out = _chunk_prepared(gpu_ops, case, pool, dev)
+    ref_pool = C.clone_pool(case.pool)
+    ref = R.kda_chunk(case.q.float() * case.scale, case.k, case.v, case.g, case.beta,
+                      state_pool=ref_pool, state_indices=case.indices,
+                      cu_seqlens=case.cu_seqlens, out_dtype=torch.float32)
+    C.assert_out(out.cpu(), ref, C.OUT_TOL, "output")
+    C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, "pool")
+    used = set(s for s in indices if s > 0)
+    other = [s for s in range(slots) if s not in used]
+    assert torch.equal(pool.cpu()[other], case.pool[other]), "an unused slot was written"
+
+
 @pytest.mark.parametrize("heads", [1, 2, 4])
 def test_chunk_persistent_scan_tracking_and_padding(gpu_ops, heads):
     """More (sequence, head) items than the scan has teams of workgroups (64 on
