@@ -2211,10 +2211,25 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 for (int j = 0; j < cc.nch; ++j, ++J) {
                     step(j, J & 1, gA, gA);
                 }
+                // The next item's state is taken before this item's is
+                // stored: a wait for the prefetch issued behind those stores
+                // would wait for the stores too (the wave's memory counter is
+                // in order, and the stores' branch makes it count them all).
+                const bool more = cc.k + 1 < KT;
+                f32x4 Sx[2][NT];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                    for (int ct = 0; ct < NT; ++ct) {
+                        Sx[tt][ct] = sn_zero || !more ? z4 : Sn[tt][ct];
+                        // complete here, and the stores below stay behind
+                        asm volatile("" : "+v"(Sx[tt][ct]));
+                    }
+                }
                 if (slot > 0) {
                     store_S(slot, S);
                 }
-                if (cc.k + 1 >= KT) {
+                if (!more) {
                     break;
                 }
                 cc = cn;
@@ -2223,7 +2238,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
                     for (int ct = 0; ct < NT; ++ct) {
-                        S[tt][ct] = sn_zero ? z4 : Sn[tt][ct];
+                        S[tt][ct] = Sx[tt][ct];
                     }
                 }
                 if (track_slot > 0 && track_len == 0) {
