@@ -1748,11 +1748,14 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
     // PERS: a role's position in the stream: item k (virtual chunks [base,
     // base + nch)) of sequence n and head h, its first record chunk c0 and
     // tokens [bos, eos)
+    // The next item's table entries are read from LDS when an item is
+    // entered (nx, and for the chain nx1) and used at the next item
+    // boundary, so crossing one waits on no LDS read.
     struct Cur {
         int base, k, nch, n, h, c0, bos, eos;
+        int4 nx, nx1;  // items[k + 1][0] and [1] (nx1: the chain's cursors only)
     };
-    auto cur_load = [&](Cur &c, int k) {
-        const int4 e = items[k][0];
+    auto cur_set = [&](Cur &c, int k, const int4 e, bool with1) {
         c.k = k;
         c.n = __builtin_amdgcn_readfirstlane(e.x >> 16);
         c.h = __builtin_amdgcn_readfirstlane(e.x & 0xffff);
@@ -1760,10 +1763,16 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         c.bos = __builtin_amdgcn_readfirstlane(e.z);
         c.eos = __builtin_amdgcn_readfirstlane(e.w);
         c.nch = (c.eos - c.bos + BT - 1) / BT;
+        const int kn = k + 1 < KA ? k + 1 : k;
+        c.nx = items[kn][0];
+        if (with1) {
+            c.nx1 = items[kn][1];
+        }
     };
-    auto cur_init = [&](Cur &c) {
+    auto cur_load = [&](Cur &c, int k, bool with1 = false) { cur_set(c, k, items[k][0], with1); };
+    auto cur_init = [&](Cur &c, bool with1 = false) {
         c.base = 0;
-        cur_load(c, 0);
+        cur_load(c, 0, with1);
     };
     // local chunk of virtual chunk J (clamped to the stream's last), moving c
     // forward (the calls at one site never go back)
@@ -1771,7 +1780,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
         J = J < j1 ? J : j1 - 1;
         while (J >= c.base + c.nch && c.k + 1 < KT) {
             c.base += c.nch;
-            cur_load(c, c.k + 1);
+            cur_set(c, c.k + 1, c.nx, false);
         }
         return J - c.base;
     };
@@ -2144,12 +2153,12 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             bool sn_zero = false;  // the next item has no state: Sn is a dummy load
             // the chain's context of item c: sequence, head, tokens, and the
             // slots from the table (no global loads at an item change)
-            auto enter = [&](const Cur &c) {
+            int4 cn1;  // items[cn.k][1]
+            auto enter = [&](const Cur &c, const int4 e) {
                 n = c.n;
                 h = c.h;
                 bos = c.bos;
                 eos = c.eos;
-                const int4 e = items[c.k][1];
                 slot = __builtin_amdgcn_readfirstlane(e.x);
                 track_slot = __builtin_amdgcn_readfirstlane(e.y);
                 track_len = __builtin_amdgcn_readfirstlane(e.z);
@@ -2163,8 +2172,9 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             auto prefetch = [&]() {
                 if (cc.k + 1 < KT) {
                     cn.base = cc.base + cc.nch;
-                    cur_load(cn, cc.k + 1);
-                    const int ns = __builtin_amdgcn_readfirstlane(items[cn.k][1].x);
+                    cur_set(cn, cc.k + 1, cc.nx, true);
+                    cn1 = cc.nx1;
+                    const int ns = __builtin_amdgcn_readfirstlane(cn1.x);
                     sn_zero = ns == 0;
                     const float *src = sn_zero ? reinterpret_cast<const float *>(ws + LY.recs)
                                                : a.state + ns * a.state_stride_slot +
@@ -2181,8 +2191,8 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                 }
             };
             if (j1 > 0) {
-                cur_init(cc);
-                enter(cc);
+                cur_init(cc, true);
+                enter(cc, items[0][1]);
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
@@ -2233,7 +2243,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
                     break;
                 }
                 cc = cn;
-                enter(cc);
+                enter(cc, cn1);
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
@@ -2253,7 +2263,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const KdaChunk
             for (int k = KT; k < KA; ++k) {
                 Cur ce;
                 cur_load(ce, k);
-                enter(ce);
+                enter(ce, items[k][1]);
                 if (track_slot > 0 && track_len == 0) {
 #pragma unroll
                     for (int tt = 0; tt < 2; ++tt) {
