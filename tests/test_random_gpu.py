@@ -4,7 +4,8 @@ Each case draws a head count on either side of the chunk scan's 16/32-column
 switch (more than 32 (sequence, head) chains run 32-column scan groups on a
 256-CU part), 1-6 sequences whose lengths favour chunk boundaries (1, 63, 64,
 65, 127, 128, 129 tokens, or any length up to 300; in the prefill forms some
-sequences are empty), state slots with the
+sequences are empty; one chunk set draws 9-80 sequences, enough chains for the
+persistent scan), state slots with the
 padding slot 0 mixed in, and, for most cases, a tracked prefix per sequence
 into its own distinct slot (sometimes none, i.e. track slot 0). The chunk op is
 checked against ``oracle.kda_ref.kda_chunk`` and the recurrent op against
@@ -29,10 +30,16 @@ HEADS = (1, 2, 3, 5, 8, 17, 33, 40)
 LENGTHS = (1, 2, 63, 64, 65, 127, 128, 129)
 
 
-def _draw(seed, max_len=300, track_prob=0.6, empty_prob=0.0):
+def _draw(seed, max_len=300, track_prob=0.6, empty_prob=0.0, many=False):
     rng = random.Random(seed)
     heads = rng.choice(HEADS)
-    n = rng.randint(1, 6)
+    if many:
+        # 9-80 sequences with more (sequence, head) chains than the 64 scan
+        # teams of a 256-CU part: the persistent scan's item streams (at most
+        # about 20k token-heads, so the oracle stays quick)
+        n = rng.randint(max(9, 65 // heads + 1), max(9, min(80, 20000 // (heads * 128))))
+    else:
+        n = rng.randint(1, 6)
     lengths = [rng.choice(LENGTHS) if rng.random() < 0.6 else rng.randint(1, max_len)
                for _ in range(n)]
     lengths = [0 if rng.random() < empty_prob else min(x, max_len) for x in lengths]
@@ -60,12 +67,11 @@ def _prepared(case):
                          case.lower_bound, case.scale)
 
 
-@pytest.mark.parametrize("seed", range(16))
-def test_random_chunk_matches_oracle(gpu_ops, seed):
-    heads, lengths, slots, indices, track = _draw(1000 + seed, empty_prob=0.1)
-    label = f"seed {seed}: H={heads} lengths={lengths} indices={indices} track={track}"
+def _check_chunk(gpu_ops, draw, case_seed, label):
+    heads, lengths, slots, indices, track = draw
+    label = f"{label}: H={heads} lengths={lengths} indices={indices} track={track}"
     print(label, flush=True)
-    case = C.raw_case(heads, lengths, indices=indices, slots=slots, seed=7000 + seed, track=track)
+    case = C.raw_case(heads, lengths, indices=indices, slots=slots, seed=case_seed, track=track)
     pool = C.to_dev(case.pool, DEV)
     out = gpu_ops.kda_varlen_chunk(prefill=True, **case.kwargs(DEV, pool=pool))
     torch.cuda.synchronize()
@@ -78,6 +84,17 @@ def test_random_chunk_matches_oracle(gpu_ops, seed):
     C.assert_rel(pool.cpu(), ref_pool, C.STATE_TOL, f"{label} pool")
     other = _untouched(case, indices, track, slots)
     assert torch.equal(pool.cpu()[other], case.pool[other]), f"{label}: an unused slot was written"
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_chunk_matches_oracle(gpu_ops, seed):
+    _check_chunk(gpu_ops, _draw(1000 + seed, empty_prob=0.1), 7000 + seed, f"seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_chunk_many_sequences(gpu_ops, seed):
+    _check_chunk(gpu_ops, _draw(3000 + seed, max_len=400, empty_prob=0.05, many=True), 10000 + seed,
+                 f"many-sequence seed {seed}")
 
 
 @pytest.mark.parametrize("seed", range(12))
