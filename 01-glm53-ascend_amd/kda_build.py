@@ -47,6 +47,12 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # Multiply-adds fuse only within one source expression: every template
+    # instantiation of a kernel then rounds the same way, so the chunk scan's
+    # one-pass, windowed and persistent forms agree bit for bit (with
+    # contraction across statements they differed in the last bit of some
+    # state elements at 32-column groups).
+    "-ffp-contract=on",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -55,20 +55,23 @@ def _launch(lib, case, nbytes, track=None):
     return rc, out, pool
 
 
-@pytest.mark.parametrize("label,lens,bounds,window,track", [
-    ("five-chunk segments", (4096,), None, 5, None),
-    ("ragged, track across", (4096,), (37, 4096 - 42), 7, (3, 1500)),
-    ("one-chunk segments", (1024,), None, 1, (3, 640)),
-    ("window of the whole", (1024,), None, 16, None),
+@pytest.mark.parametrize("label,heads,lens,bounds,window,track", [
+    ("five-chunk segments", 8, (4096,), None, 5, None),
+    ("ragged, track across", 8, (4096,), (37, 4096 - 42), 7, (3, 1500)),
+    ("one-chunk segments", 8, (1024,), None, 1, (3, 640)),
+    ("window of the whole", 8, (1024,), None, 16, None),
+    # more than 32 heads: 32-column scan groups on a 256-CU part
+    ("32-column groups", 40, (4096,), (1, 4096 - 5), 30, (3, 1101)),
+    ("32-column groups, one chunk", 40, (64,), None, 1, None),
 ])
-def test_small_workspace_runs_segments(label, lens, bounds, window, track):
+def test_small_workspace_runs_segments(label, heads, lens, bounds, window, track):
     """A workspace below kda_chunk_workspace_bytes but holding `window` records
     per head runs the sequence in segments of that many chunks, one after
     another, bit for bit equal to the one-pass launch."""
     import dataclasses
 
     lib = _lib()
-    case = C.prepared_case(8, lens, slots=4, indices=[2], seed=91 + len(label))
+    case = C.prepared_case(heads, lens, slots=4, indices=[2], seed=91 + len(label))
     if bounds is not None:
         case = dataclasses.replace(case, cu_seqlens=torch.tensor(bounds, dtype=torch.int32))
     T, H, D = case.q.shape[1:]
