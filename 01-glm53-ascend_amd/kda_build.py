@@ -47,15 +47,15 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
-    # Multiply-adds fuse only within one source expression: every template
-    # instantiation of a kernel then rounds the same way, so the chunk scan's
-    # one-pass, windowed and persistent forms agree bit for bit (with
-    # contraction across statements they differed in the last bit of some
-    # state elements at 32-column groups).
-    "-ffp-contract=on",
     "-Wall",
     "-Wno-unused-function",
 ]
+# The chunk kernels fuse multiply-adds only within one source expression:
+# every template instantiation then rounds the same way, so the scan's
+# one-pass, windowed and persistent forms agree bit for bit (with contraction
+# across statements they differed in the last bit of some state elements at
+# 32-column groups). The recurrent kernel keeps the default.
+SOURCE_FLAGS = {"kda_chunk.hip": ["-ffp-contract=on"]}
 
 
 def _run(cmd, verbose):
@@ -125,7 +125,7 @@ def build(verbose: bool = False, out_dir: str = PKG) -> None:
             obj = os.path.join(obj_dir, src + ".o")
             objs.append(obj)
             lang = [] if src.endswith(".hip") else ["-x", "hip"]
-            cmd = [HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *lang, "-c",
+            cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", *lang, "-c",
                    os.path.join(CSRC, src), "-o", obj]
             if verbose:
                 print(" ".join(cmd), flush=True)
